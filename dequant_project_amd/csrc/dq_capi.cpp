@@ -1,0 +1,297 @@
+// C ABI of the fused dequant + GEMV engine (declared in include/dequant_hip.h).
+//
+// Two layers:
+//   dq_check_*  validate operand descriptors in the order, and with the
+//               messages, of the reference's host code
+//               (kernels/dequant_gemv.cu:230-283 check_weight, :310-317
+//               dequantize, :342-361 gemv). Pure host logic: no HIP call, so
+//               they run on machines without a GPU.
+//   dq_gemv / dq_dequantize / dq_unpack / dq_add_one
+//               validate the scalar contract of a raw-pointer call (the rules
+//               that do not need tensor metadata) and launch on `stream`.
+// Errors are reported as a status code plus a thread-local message.
+
+#include <cstdint>
+#include <cstring>
+#include <sstream>
+#include <string>
+
+#include "dequant_hip.h"
+#include "dq_internal.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int status, const std::string& msg) {
+  g_error = msg;
+  return status;
+}
+
+template <typename... Ts>
+std::string cat(const Ts&... parts) {
+  std::ostringstream os;
+  (os << ... << parts);
+  return os.str();
+}
+
+// torch's IntArrayRef formatting: "[a, b, c]"
+std::string sizes_str(const dq_tensor* t) {
+  std::ostringstream os;
+  os << "[";
+  for (int i = 0; i < t->ndim && i < 4; ++i) os << (i ? ", " : "") << t->sizes[i];
+  os << "]";
+  return os.str();
+}
+
+bool same_sizes(const dq_tensor* a, const dq_tensor* b) {
+  if (a->ndim != b->ndim) return false;
+  for (int i = 0; i < a->ndim && i < 4; ++i)
+    if (a->sizes[i] != b->sizes[i]) return false;
+  return true;
+}
+
+bool same_device(const dq_tensor* a, const dq_tensor* b) {
+  return a->is_device == b->is_device && (!a->is_device || a->device == b->device);
+}
+
+constexpr int64_t kMaxDim = int64_t(1) << 30;  // kernel index arithmetic stays in range
+
+// kernels/dequant_gemv.cu:233-238
+int check_bits_group_k(int64_t bits, int64_t group_size, int64_t K) {
+  if (!(bits == 2 || bits == 4 || bits == 8))
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("bits must be 2, 4 or 8, got ", bits));
+  if (group_size <= 0)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("group_size must be positive, got ", group_size));
+  if (!(K > 0 && K % group_size == 0))
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("K=", K, " is not divisible by group_size=", group_size));
+  return DQ_OK;
+}
+
+// kernels/dequant_gemv.cu:259-261
+int check_zeros_presence(bool has_zeros, bool symmetric) {
+  if (has_zeros != !symmetric)
+    return fail(DQ_ERR_INVALID_ARGUMENT,
+                symmetric ? "symmetric=true takes no zeros" : "symmetric=false requires zeros");
+  return DQ_OK;
+}
+
+// kernels/dequant_gemv.cu:240-246
+int check_qweight(const dq_tensor* qw, int64_t bits, int64_t K) {
+  const int64_t per = 32 / bits;
+  if (!qw->is_device) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be a CUDA tensor");
+  if (qw->dtype != DQ_DTYPE_INT32) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be int32");
+  if (!qw->contiguous) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be contiguous");
+  if (qw->ndim != 2) return fail(DQ_ERR_INVALID_ARGUMENT, cat("qweight must be 2-D, got ", qw->ndim, "-D"));
+  if (qw->sizes[1] * per != K)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("qweight has ", qw->sizes[1], " words per row, which is ",
+                                             qw->sizes[1] * per, " codes, but K=", K));
+  return DQ_OK;
+}
+
+// check_weight, kernels/dequant_gemv.cu:230-283
+int check_weight(const dq_tensor* qw, const dq_tensor* sc, const dq_tensor* ze, int64_t bits,
+                 int64_t group_size, bool symmetric, int64_t K) {
+  int st = check_bits_group_k(bits, group_size, K);
+  if (st) return st;
+  if ((st = check_qweight(qw, bits, K))) return st;
+
+  const int64_t N = qw->sizes[0];
+  const int64_t n_groups = K / group_size;
+  if (!sc->is_device) return fail(DQ_ERR_INVALID_ARGUMENT, "scales must be a CUDA tensor");
+  if (sc->dtype != DQ_DTYPE_FLOAT16) return fail(DQ_ERR_INVALID_ARGUMENT, "scales must be float16");
+  if (!sc->contiguous) return fail(DQ_ERR_INVALID_ARGUMENT, "scales must be contiguous");
+  if (!(sc->ndim == 2 && sc->sizes[0] == N && sc->sizes[1] == n_groups))
+    return fail(DQ_ERR_INVALID_ARGUMENT,
+                cat("scales must be [", N, ", ", n_groups, "], got ", sizes_str(sc)));
+  if (!same_device(sc, qw))
+    return fail(DQ_ERR_INVALID_ARGUMENT, "scales and qweight must be on the same device");
+
+  if ((st = check_zeros_presence(ze != nullptr, symmetric))) return st;
+  if (ze) {
+    if (!ze->is_device) return fail(DQ_ERR_INVALID_ARGUMENT, "zeros must be a CUDA tensor");
+    if (ze->dtype != DQ_DTYPE_FLOAT16) return fail(DQ_ERR_INVALID_ARGUMENT, "zeros must be float16");
+    if (!ze->contiguous) return fail(DQ_ERR_INVALID_ARGUMENT, "zeros must be contiguous");
+    if (!same_sizes(ze, sc))
+      return fail(DQ_ERR_INVALID_ARGUMENT, cat("zeros must have the same shape as scales, got ", sizes_str(ze)));
+    if (!same_device(ze, qw))
+      return fail(DQ_ERR_INVALID_ARGUMENT, "zeros and qweight must be on the same device");
+  }
+  return DQ_OK;
+}
+
+// kernels/dequant_gemv.cu:357-361
+int check_gemv_group(int64_t group_size, int64_t bits) {
+  const int64_t cpl = 128 / bits;
+  if (group_size % cpl != 0)
+    return fail(DQ_ERR_INVALID_ARGUMENT,
+                cat("group_size=", group_size, " must be a multiple of ", cpl,
+                    " (the codes one lane loads per uint4) at ", bits,
+                    " bits; this excludes INT2 with group_size 32"));
+  return DQ_OK;
+}
+
+// kernels/dequant_gemv.cu:315-317
+int check_dequant_group(int64_t group_size, int64_t bits) {
+  const int64_t per = 32 / bits;
+  if (group_size % per != 0)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("group_size=", group_size, " must be a multiple of ", per,
+                                             " values per uint32 word at ", bits, " bits"));
+  return DQ_OK;
+}
+
+// kernels/dequant_gemv.cu:349-350
+int check_m(int64_t M) {
+  if (!(M >= 1 && M <= DQ_MAX_M))
+    return fail(DQ_ERR_UNSUPPORTED, cat("gemv handles 1 <= M <= ", DQ_MAX_M, ", got M=", M,
+                                        "; use the dequantize + F.linear fallback"));
+  return DQ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Limits of this implementation (no reference counterpart: the reference's
+// kernels index with int and would overflow silently).
+int check_extent(int64_t N, int64_t K) {
+  if (N < 0) return fail(DQ_ERR_INVALID_ARGUMENT, cat("N must be non-negative, got ", N));
+  if (N >= (int64_t(1) << 31) || K > kMaxDim)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("shape [", N, ", ", K, "] exceeds the supported extent"));
+  return DQ_OK;
+}
+
+int launch_status(hipError_t e) {
+  if (e == hipSuccess) return DQ_OK;
+  return fail(DQ_ERR_LAUNCH, cat("HIP launch failed: ", hipGetErrorString(e)));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dq_last_error(void) { return g_error.c_str(); }
+
+const char* dq_status_name(int status) {
+  switch (status) {
+    case DQ_OK: return "DQ_OK";
+    case DQ_ERR_INVALID_ARGUMENT: return "DQ_ERR_INVALID_ARGUMENT";
+    case DQ_ERR_UNSUPPORTED: return "DQ_ERR_UNSUPPORTED";
+    case DQ_ERR_LAUNCH: return "DQ_ERR_LAUNCH";
+    case DQ_ERR_HIP: return "DQ_ERR_HIP";
+    default: return "DQ_ERR_UNKNOWN";
+  }
+}
+
+int dq_version(void) { return 100; }
+
+int dq_check_gemv(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor* scales,
+                  const dq_tensor* zeros, int64_t bits, int64_t group_size, int symmetric) {
+  g_error.clear();
+  if (!x || !qweight || !scales)
+    return fail(DQ_ERR_INVALID_ARGUMENT, "x, qweight and scales descriptors must not be NULL");
+  // kernels/dequant_gemv.cu:342-352
+  if (!x->is_device) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be a CUDA tensor");
+  if (x->dtype != DQ_DTYPE_FLOAT16) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be float16");
+  if (!x->contiguous) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be contiguous");
+  if (x->ndim != 2) return fail(DQ_ERR_INVALID_ARGUMENT, cat("x must be 2-D [M, K], got ", x->ndim, "-D"));
+  int st = check_m(x->sizes[0]);
+  if (st) return st;
+  if (!aligned16(x->data)) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+  const int64_t K = x->sizes[1];
+  // :354 check_weight, :355 device, :357-361 group vs. 16-byte load
+  if ((st = check_weight(qweight, scales, zeros, bits, group_size, symmetric != 0, K))) return st;
+  if (!same_device(x, qweight))
+    return fail(DQ_ERR_INVALID_ARGUMENT, "x and qweight must be on the same device");
+  if ((st = check_gemv_group(group_size, bits))) return st;
+  // this implementation's own requirements
+  if (!aligned16(qweight->data)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
+  return check_extent(qweight->sizes[0], K);
+}
+
+int dq_check_dequantize(const dq_tensor* qweight, const dq_tensor* scales, const dq_tensor* zeros,
+                        int64_t bits, int64_t group_size, int symmetric, int64_t K) {
+  g_error.clear();
+  if (!qweight || !scales)
+    return fail(DQ_ERR_INVALID_ARGUMENT, "qweight and scales descriptors must not be NULL");
+  int st = check_weight(qweight, scales, zeros, bits, group_size, symmetric != 0, K);
+  if (st) return st;
+  if ((st = check_dequant_group(group_size, bits))) return st;
+  return check_extent(qweight->sizes[0], K);
+}
+
+int dq_check_unpack(const dq_tensor* qweight, int64_t bits, int64_t K) {
+  g_error.clear();
+  if (!qweight) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight descriptor must not be NULL");
+  if (!(bits == 2 || bits == 4 || bits == 8))
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("bits must be 2, 4 or 8, got ", bits));
+  if (K <= 0 || K % (32 / bits) != 0)
+    return fail(DQ_ERR_INVALID_ARGUMENT,
+                cat("K=", K, " is not a positive multiple of ", 32 / bits, " values per word"));
+  int st = check_qweight(qweight, bits, K);
+  if (st) return st;
+  return check_extent(qweight->sizes[0], K);
+}
+
+int dq_gemv(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales, const uint16_t* zeros,
+            uint16_t* y, int64_t M, int64_t N, int64_t K, int64_t bits, int64_t group_size, int symmetric,
+            int interleaved, dq_stream_t stream) {
+  g_error.clear();
+  int st = check_m(M);
+  if (st) return st;
+  if (!x || !qweight || !scales || !y)
+    return fail(DQ_ERR_INVALID_ARGUMENT, "x, qweight, scales and y must not be NULL");
+  if (!aligned16(x)) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+  if ((st = check_bits_group_k(bits, group_size, K))) return st;
+  if ((st = check_zeros_presence(zeros != nullptr, symmetric != 0))) return st;
+  if ((st = check_gemv_group(group_size, bits))) return st;
+  if (!aligned16(qweight)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
+  if ((st = check_extent(N, K))) return st;
+  if (N == 0) return DQ_OK;
+  dq::GemvProblem p{x, qweight, scales, zeros, y, M, N, K, static_cast<int>(bits), group_size,
+                    symmetric != 0, interleaved != 0};
+  return launch_status(dq::launch_gemv(p, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dq_dequantize(const uint32_t* qweight, const uint16_t* scales, const uint16_t* zeros, uint16_t* out,
+                  int64_t N, int64_t K, int64_t bits, int64_t group_size, int symmetric, int interleaved,
+                  dq_stream_t stream) {
+  g_error.clear();
+  int st = check_bits_group_k(bits, group_size, K);
+  if (st) return st;
+  if (!qweight || !scales || !out)
+    return fail(DQ_ERR_INVALID_ARGUMENT, "qweight, scales and out must not be NULL");
+  if ((st = check_zeros_presence(zeros != nullptr, symmetric != 0))) return st;
+  if ((st = check_dequant_group(group_size, bits))) return st;
+  if (!aligned16(out)) return fail(DQ_ERR_INVALID_ARGUMENT, "out must be 16-byte aligned");
+  if ((st = check_extent(N, K))) return st;
+  if (N == 0) return DQ_OK;
+  dq::DequantProblem p{qweight, scales, zeros, out, N, K, static_cast<int>(bits), group_size,
+                       symmetric != 0, interleaved != 0};
+  return launch_status(dq::launch_dequantize(p, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dq_unpack(const uint32_t* qweight, int32_t* out, int64_t N, int64_t K, int64_t bits, int interleaved,
+              dq_stream_t stream) {
+  g_error.clear();
+  if (!(bits == 2 || bits == 4 || bits == 8))
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("bits must be 2, 4 or 8, got ", bits));
+  if (K <= 0 || K % (32 / bits) != 0)
+    return fail(DQ_ERR_INVALID_ARGUMENT,
+                cat("K=", K, " is not a positive multiple of ", 32 / bits, " values per word"));
+  if (!qweight || !out) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight and out must not be NULL");
+  if (!aligned16(out)) return fail(DQ_ERR_INVALID_ARGUMENT, "out must be 16-byte aligned");
+  int st = check_extent(N, K);
+  if (st) return st;
+  if (N == 0) return DQ_OK;
+  return launch_status(dq::launch_unpack(qweight, out, N, K, static_cast<int>(bits), interleaved != 0,
+                                         reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dq_add_one(const float* in, float* out, int64_t n, dq_stream_t stream) {
+  g_error.clear();
+  if (n < 0) return fail(DQ_ERR_INVALID_ARGUMENT, cat("n must be non-negative, got ", n));
+  if (n == 0) return DQ_OK;
+  if (!in || !out) return fail(DQ_ERR_INVALID_ARGUMENT, "in and out must not be NULL");
+  return launch_status(dq::launch_add_one(in, out, n, reinterpret_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

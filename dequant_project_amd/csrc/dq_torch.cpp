@@ -1,0 +1,119 @@
+// PyTorch-ROCm extension `dequant_cuda`: the reference's Python surface
+// (kernels/bindings.cpp:5-17, prototypes kernels/dequant_cuda.h:10-20) over the
+// C ABI of include/dequant_hip.h. This layer only turns tensors into operand
+// descriptors, allocates outputs (as the reference's launchers do with
+// torch::empty) and picks the current HIP stream; validation and launches
+// live behind the C ABI. Errors raise RuntimeError with the reference's text.
+
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <optional>
+#include <stdexcept>
+
+#include "dequant_hip.h"
+
+namespace {
+
+dq_tensor describe(const at::Tensor& t) {
+  dq_tensor d{};
+  d.data = t.data_ptr();
+  d.is_device = t.is_cuda() ? 1 : 0;
+  d.device = t.is_cuda() ? t.get_device() : -1;
+  switch (t.scalar_type()) {
+    case at::kInt: d.dtype = DQ_DTYPE_INT32; break;
+    case at::kHalf: d.dtype = DQ_DTYPE_FLOAT16; break;
+    case at::kFloat: d.dtype = DQ_DTYPE_FLOAT32; break;
+    default: d.dtype = DQ_DTYPE_OTHER; break;
+  }
+  d.contiguous = t.is_contiguous() ? 1 : 0;
+  d.ndim = static_cast<int32_t>(t.dim());
+  for (int i = 0; i < d.ndim && i < 4; ++i) d.sizes[i] = t.size(i);
+  return d;
+}
+
+void raise_if(int status) {
+  if (status != DQ_OK) throw std::runtime_error(dq_last_error());
+}
+
+dq_stream_t current_stream(const at::Tensor& t) {
+  return reinterpret_cast<dq_stream_t>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+const uint16_t* half_ptr(const at::Tensor& t) { return reinterpret_cast<const uint16_t*>(t.data_ptr()); }
+
+}  // namespace
+
+// kernels/smoke.cu:15-25
+torch::Tensor add_one(torch::Tensor x) {
+  if (!x.is_cuda()) throw std::runtime_error("x must be a CUDA tensor");
+  if (x.scalar_type() != at::kFloat) throw std::runtime_error("x must be float32");
+  auto xc = x.contiguous();
+  const c10::DeviceGuard guard(x.device());
+  auto out = torch::empty_like(xc);
+  raise_if(dq_add_one(xc.data_ptr<float>(), out.data_ptr<float>(), xc.numel(), current_stream(xc)));
+  return out;
+}
+
+// kernels/dequant_gemv.cu:339-386
+torch::Tensor gemv(torch::Tensor x, torch::Tensor qweight, torch::Tensor scales,
+                   std::optional<torch::Tensor> zeros, int64_t bits, int64_t group_size, bool symmetric,
+                   bool interleaved) {
+  const dq_tensor dx = describe(x), dw = describe(qweight), ds = describe(scales);
+  dq_tensor dz{};
+  if (zeros) dz = describe(*zeros);
+  raise_if(dq_check_gemv(&dx, &dw, &ds, zeros ? &dz : nullptr, bits, group_size, symmetric));
+
+  const c10::DeviceGuard guard(x.device());
+  const int64_t M = x.size(0), K = x.size(1), N = qweight.size(0);
+  auto y = torch::empty({M, N}, x.options());
+  raise_if(dq_gemv(half_ptr(x), reinterpret_cast<const uint32_t*>(qweight.data_ptr()), half_ptr(scales),
+                   zeros ? half_ptr(*zeros) : nullptr, reinterpret_cast<uint16_t*>(y.data_ptr()), M, N, K, bits,
+                   group_size, symmetric, interleaved, current_stream(x)));
+  return y;
+}
+
+// kernels/dequant_gemv.cu:310-337
+torch::Tensor dequantize(torch::Tensor qweight, torch::Tensor scales, std::optional<torch::Tensor> zeros,
+                         int64_t bits, int64_t group_size, bool symmetric, bool interleaved, int64_t K) {
+  const dq_tensor dw = describe(qweight), ds = describe(scales);
+  dq_tensor dz{};
+  if (zeros) dz = describe(*zeros);
+  raise_if(dq_check_dequantize(&dw, &ds, zeros ? &dz : nullptr, bits, group_size, symmetric, K));
+
+  const c10::DeviceGuard guard(qweight.device());
+  const int64_t N = qweight.size(0);
+  auto out = torch::empty({N, K}, scales.options());
+  raise_if(dq_dequantize(reinterpret_cast<const uint32_t*>(qweight.data_ptr()), half_ptr(scales),
+                         zeros ? half_ptr(*zeros) : nullptr, reinterpret_cast<uint16_t*>(out.data_ptr()), N, K,
+                         bits, group_size, symmetric, interleaved, current_stream(qweight)));
+  return out;
+}
+
+// No reference counterpart: the codes themselves, for the bit-exact unpack check
+// against dequant/packer.py:164-174.
+torch::Tensor unpack(torch::Tensor qweight, int64_t bits, bool interleaved, int64_t K) {
+  const dq_tensor dw = describe(qweight);
+  raise_if(dq_check_unpack(&dw, bits, K));
+  const c10::DeviceGuard guard(qweight.device());
+  const int64_t N = qweight.size(0);
+  auto out = torch::empty({N, K}, qweight.options().dtype(at::kInt));
+  raise_if(dq_unpack(reinterpret_cast<const uint32_t*>(qweight.data_ptr()), out.data_ptr<int32_t>(), N, K,
+                     bits, interleaved, current_stream(qweight)));
+  return out;
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("add_one", &add_one, "add one (HIP, gfx950)", py::arg("x"));
+  m.def("gemv", &gemv, "packed-weight GEMV, fp16 [M,K] x [N,K]^T -> [M,N]", py::arg("x"), py::arg("qweight"),
+        py::arg("scales"), py::arg("zeros"), py::arg("bits"), py::arg("group_size"), py::arg("symmetric"),
+        py::arg("interleaved"));
+  m.def("dequantize", &dequantize, "materialize a packed weight as fp16 [N,K]", py::arg("qweight"),
+        py::arg("scales"), py::arg("zeros"), py::arg("bits"), py::arg("group_size"), py::arg("symmetric"),
+        py::arg("interleaved"), py::arg("K"));
+  m.def("unpack", &unpack, "packed words -> int32 codes [N,K] in logical order", py::arg("qweight"),
+        py::arg("bits"), py::arg("interleaved"), py::arg("K"));
+  m.attr("library_version") = dq_version();
+}

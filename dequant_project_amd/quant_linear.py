@@ -1,0 +1,118 @@
+"""QuantLinear: an nn.Linear drop-in whose weight exists only in packed form.
+
+Public surface of the reference's dequant/quant_linear.py (MAX_M :39, PROJ
+:44, _get_ext :49-69, gemv :72-82, dequantize_cuda :85-93, QuantLinear
+:96-140, quantize_model :143-162), backed by the gfx950 engine:
+
+  M <= MAX_M   the fused dequant + GEMV kernel (dequant_cuda.gemv): codes are
+               unpacked in registers, nothing is materialized. The decode path.
+  M >  MAX_M   dequant_cuda.dequantize materializes the fp16 [N, K] weight
+               (bit-exact with packer.dequantize) and F.linear does the GEMM.
+
+Both branches launch on the current HIP stream and never synchronize, so a
+forward pass can be captured into a HIP graph (torch.cuda.CUDAGraph). There is
+no CPU or pure-torch fallback: without the built extension `_get_ext()`
+raises ImportError.
+"""
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import _native
+from .packer import PackedWeight, QuantConfig, quantize_tensor
+
+# Largest batch the fused kernel handles; above it the dequantize fallback runs.
+MAX_M = 8
+
+# The projections of a Llama-style decoder layer that quantize_model replaces.
+PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def _get_ext():
+    """The `dequant_cuda` extension module; ImportError with a build hint if absent."""
+    return _native.ext()
+
+
+def gemv(x, pw: PackedWeight):
+    """y = x @ W^T with W packed. x fp16 [..., K] -> y fp16 [..., N]."""
+    n, k = pw.shape
+    cfg = pw.config
+    x2 = x.reshape(-1, k).contiguous()
+    y = _get_ext().gemv(x2, pw.qweight, pw.scales, pw.zeros, cfg.bits,
+                        cfg.effective_group_size(k), cfg.symmetric,
+                        cfg.layout == "interleaved")
+    return y.view(*x.shape[:-1], n)
+
+
+def dequantize_cuda(pw: PackedWeight):
+    """fp16 [N, K] on the GPU, bit-exact with packer.dequantize."""
+    n, k = pw.shape
+    cfg = pw.config
+    return _get_ext().dequantize(pw.qweight, pw.scales, pw.zeros, cfg.bits,
+                                 cfg.effective_group_size(k), cfg.symmetric,
+                                 cfg.layout == "interleaved", k)
+
+
+class QuantLinear(nn.Module):
+    """nn.Linear replacement holding only qweight / scales / zeros (+ bias) buffers.
+
+    There is deliberately no `.weight`, so nothing can fall back to an fp16
+    matmul over a full-size weight.
+    """
+
+    def __init__(self, pw: PackedWeight, bias=None):
+        super().__init__()
+        self.out_features, self.in_features = pw.shape
+        self.config = pw.config
+        self.register_buffer("qweight", pw.qweight)
+        self.register_buffer("scales", pw.scales)
+        self.register_buffer("zeros", pw.zeros)
+        self.register_buffer("bias", bias)
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, cfg: QuantConfig):
+        pw = quantize_tensor(linear.weight.data, cfg)
+        bias = None if linear.bias is None else linear.bias.data.to(torch.float16)
+        return cls(pw, bias)
+
+    def _packed(self):
+        # Rebuilt on every call so that .to() / .cuda() moves stay visible.
+        return PackedWeight(qweight=self.qweight, scales=self.scales, zeros=self.zeros,
+                            config=self.config, shape=(self.out_features, self.in_features))
+
+    def forward(self, x):
+        pw = self._packed()
+        m = x.numel() // self.in_features
+        if m <= MAX_M:
+            y = gemv(x, pw)
+        else:
+            y = F.linear(x, dequantize_cuda(pw))
+        if self.bias is not None:
+            y = y + self.bias
+        return y
+
+    def extra_repr(self):
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, config={self.config}")
+
+
+def quantize_model(model, cfg: QuantConfig, names=PROJ):
+    """Swap every nn.Linear whose leaf name is in `names` for a QuantLinear, in place.
+
+    Returns {"replaced", "packed_bytes", "fp16_bytes"}.
+    """
+    replaced = packed_bytes = fp16_bytes = 0
+    for path, mod in list(model.named_modules()):
+        leaf = path.rsplit(".", 1)[-1]
+        if leaf not in names or not isinstance(mod, nn.Linear):
+            continue
+        parent = model.get_submodule(path.rsplit(".", 1)[0] if "." in path else "")
+        ql = QuantLinear.from_linear(mod, cfg)
+        setattr(parent, leaf, ql)
+        replaced += 1
+        packed_bytes += ql._packed().nbytes
+        fp16_bytes += mod.weight.numel() * 2
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
+    return {"replaced": replaced, "packed_bytes": packed_bytes, "fp16_bytes": fp16_bytes}

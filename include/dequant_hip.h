@@ -1,0 +1,157 @@
+/*
+ * dequant_hip.h -- C ABI of the MI355X (gfx950) fused dequant + GEMV engine.
+ *
+ * This is the drop-in boundary for the decode path of the reference project
+ * (KrishnaI2424/Dequant_Project). The reference binds three C++ launchers into
+ * the pybind11 module `dequant_cuda`:
+ *
+ *   add_one(x)                                   kernels/dequant_cuda.h:10,  kernels/smoke.cu:15-25
+ *   gemv(x, qweight, scales, zeros, bits,
+ *        group_size, symmetric, interleaved)     kernels/dequant_cuda.h:13-15, kernels/dequant_gemv.cu:339-386
+ *   dequantize(qweight, scales, zeros, bits,
+ *              group_size, symmetric,
+ *              interleaved, K)                   kernels/dequant_cuda.h:18-20, kernels/dequant_gemv.cu:310-337
+ *   (module definition: kernels/bindings.cpp:5-17)
+ *
+ * Each is replaced below by an `extern "C"` entry point over plain device
+ * pointers and sizes. No torch types cross this boundary; a torch extension,
+ * ctypes, cgo or any other FFI can bind it. Nothing here allocates device
+ * memory: the caller owns every buffer, as the reference's callers own the
+ * tensors they pass (and the torch layer allocates the outputs, as the
+ * reference's launchers do with torch::empty).
+ *
+ * Packed format (frozen; defined by the reference's dequant/packer.py:1-201):
+ *   - a weight is [N, K]; the GEMV reduces over K; groups run along K;
+ *   - qweight is [N, K / (32/bits)] 32-bit words (torch int32 holding the
+ *     uint32 bit pattern, packer.py:159-161);
+ *   - codes are unsigned; symmetric codes are pre-biased by 2^(bits-1);
+ *   - "sequential": logical code i of a word sits at bit offset bits*i;
+ *     "interleaved": slot s holds logical code T[s] with
+ *        T4 = {0,2,4,6,1,3,5,7}, T2 = {0,4,8,12,1,5,9,13,2,6,10,14,3,7,11,15},
+ *        T8 = {0,2,1,3}                               (packer.py:37-41);
+ *   - scales (and zeros when asymmetric) are fp16 [N, K / group_size];
+ *     per-channel quantization is passed as group_size == K
+ *     (dequant/quant_linear.py:79).
+ *
+ * fp16 values travel as uint16_t bit patterns.
+ *
+ * Errors: every entry point returns DQ_OK (0) or a DQ_ERR_* status and
+ * records a message (the reference's TORCH_CHECK text, e.g.
+ * "gemv handles 1 <= M <= 8, got M=9; use the dequantize + F.linear fallback")
+ * retrievable with dq_last_error() on the calling thread. Launch errors from
+ * the HIP runtime come back as DQ_ERR_LAUNCH. Device-side faults surface
+ * asynchronously, as with any HIP launch.
+ *
+ * Streams: every launch is asynchronous on `stream` (NULL = the legacy default
+ * stream). No entry point synchronizes, allocates or reads device memory on
+ * the host, so all of them may be captured into a HIP graph.
+ */
+#ifndef DEQUANT_HIP_H_
+#define DEQUANT_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as hipStream_t (hip_runtime_api.h: typedef struct ihipStream_t* hipStream_t). */
+typedef struct ihipStream_t* dq_stream_t;
+
+enum dq_status {
+  DQ_OK = 0,
+  DQ_ERR_INVALID_ARGUMENT = 1, /* violates the packed format or the call contract */
+  DQ_ERR_UNSUPPORTED = 2,      /* well-formed, but outside what the entry point handles (M > 8) */
+  DQ_ERR_LAUNCH = 3,           /* the HIP runtime rejected a launch */
+  DQ_ERR_HIP = 4               /* another HIP runtime call failed */
+};
+
+/* Largest batch (rows of x) the fused GEMV handles; kernels/dequant_gemv.cu:27
+ * and dequant/quant_linear.py:39 (MAX_M = 8). */
+#define DQ_MAX_M 8
+
+/* Message describing the last non-OK status returned on this thread
+ * (empty string if none). Valid until the next call on this thread. */
+const char* dq_last_error(void);
+
+/* Short name of a status code ("DQ_OK", "DQ_ERR_INVALID_ARGUMENT", ...). */
+const char* dq_status_name(int status);
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int dq_version(void);
+
+/* ---------------------------------------------------------------- tensors
+ * Host-side description of one operand, used by dq_check_* to run the
+ * reference's argument validation (kernels/dequant_gemv.cu:230-283, 310-317,
+ * 342-361) in the reference's order and with the reference's messages. A
+ * binding fills one per tensor; the checks read no device memory and make no
+ * HIP call, so they run on machines without a GPU.
+ */
+enum dq_dtype { DQ_DTYPE_OTHER = 0, DQ_DTYPE_INT32 = 1, DQ_DTYPE_FLOAT16 = 2, DQ_DTYPE_FLOAT32 = 3 };
+
+typedef struct dq_tensor {
+  const void* data;   /* first element */
+  int32_t is_device;  /* 1 if the memory is GPU memory ("a CUDA tensor" in torch terms) */
+  int32_t device;     /* device ordinal when is_device */
+  int32_t dtype;      /* enum dq_dtype */
+  int32_t contiguous; /* 1 if row-major dense */
+  int32_t ndim;
+  int64_t sizes[4];   /* sizes[0..ndim-1] */
+} dq_tensor;
+
+/* Validation of dequant_cuda.gemv(x, qweight, scales, zeros, bits, group_size,
+ * symmetric, interleaved): kernels/dequant_gemv.cu:342-361 then check_weight
+ * :230-283. `zeros` may be NULL (= None). */
+int dq_check_gemv(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor* scales,
+                  const dq_tensor* zeros, int64_t bits, int64_t group_size, int symmetric);
+
+/* Validation of dequant_cuda.dequantize(..., K): kernels/dequant_gemv.cu:310-317
+ * with check_weight :230-283. */
+int dq_check_dequantize(const dq_tensor* qweight, const dq_tensor* scales, const dq_tensor* zeros,
+                        int64_t bits, int64_t group_size, int symmetric, int64_t K);
+
+/* Validation of dq_unpack's arguments (no reference counterpart; it applies
+ * the qweight rules of check_weight, kernels/dequant_gemv.cu:233-246). */
+int dq_check_unpack(const dq_tensor* qweight, int64_t bits, int64_t K);
+
+/* ---------------------------------------------------------------- compute */
+
+/* y[M, N] = fp16_rn( x[M, K] @ W^T ), W held packed; fp32 accumulation.
+ * Replaces dequant_cuda.gemv (kernels/dequant_gemv.cu:339-386, kernel :144-217).
+ *   x        fp16 [M, K], row-major, 16-byte aligned, 1 <= M <= DQ_MAX_M
+ *   qweight  [N, K*bits/32] words, 16-byte aligned
+ *   scales   fp16 [N, K/group_size]
+ *   zeros    fp16 [N, K/group_size] if !symmetric, else NULL
+ *   y        fp16 [M, N] output (written, never read)
+ * group_size must divide K and be a multiple of 128/bits codes (one 16-byte
+ * load), which excludes INT2 with group_size 32 (dequant_gemv.cu:357-361). */
+int dq_gemv(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
+            const uint16_t* zeros, uint16_t* y, int64_t M, int64_t N, int64_t K,
+            int64_t bits, int64_t group_size, int symmetric, int interleaved,
+            dq_stream_t stream);
+
+/* out[N, K] = fp16_rn( (code - offset) * scale ), bit-exact with the
+ * reference's packer.dequantize (dequant/packer.py:177-189). Replaces
+ * dequant_cuda.dequantize (kernels/dequant_gemv.cu:310-337, kernel :113-140).
+ * group_size must be a multiple of 32/bits (one word; :315-317).
+ * out must be 16-byte aligned. */
+int dq_dequantize(const uint32_t* qweight, const uint16_t* scales, const uint16_t* zeros,
+                  uint16_t* out, int64_t N, int64_t K, int64_t bits, int64_t group_size,
+                  int symmetric, int interleaved, dq_stream_t stream);
+
+/* out[N, K] = the unsigned codes, int32, logical order; bit-exact with the
+ * reference's packer.unpack (dequant/packer.py:164-174). No reference kernel:
+ * the reference unpacks only inside its kernels; this exposes the unpack step
+ * so that it can be checked bit for bit. out must be 16-byte aligned. */
+int dq_unpack(const uint32_t* qweight, int32_t* out, int64_t N, int64_t K, int64_t bits,
+              int interleaved, dq_stream_t stream);
+
+/* out[i] = in[i] + 1 for fp32, the toolchain smoke kernel
+ * (kernels/smoke.cu:9-25). Kept for export-surface parity. */
+int dq_add_one(const float* in, float* out, int64_t n, dq_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* DEQUANT_HIP_H_ */

@@ -1,0 +1,195 @@
+"""The C ABI on a machine without a GPU: it loads, exports what the header
+declares, and validates arguments in the reference's order with the
+reference's messages (kernels/dequant_gemv.cu:230-283, 310-317, 342-361).
+No compute call is made here."""
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from dequant_project_amd import _native
+from dequant_project_amd._native import DQ_DTYPE_FLOAT16, DQ_DTYPE_FLOAT32, DQ_DTYPE_INT32, DqTensor
+from tests._helpers import ROOT
+
+HEADER = ROOT / "include" / "dequant_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(dq_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ("dq_gemv", "dq_dequantize", "dq_unpack", "dq_add_one", "dq_check_gemv",
+                     "dq_check_dequantize", "dq_check_unpack", "dq_last_error", "dq_status_name",
+                     "dq_version"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.capi()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _native.SIGNATURES, f"{name} missing from _native.SIGNATURES"
+    assert lib.dq_version() == 100
+    assert lib.dq_status_name(0) == b"DQ_OK"
+
+
+def dev(t):
+    """Describe a CPU tensor as if it lived on GPU 0 (validation only)."""
+    d = _native.describe(t)
+    d.is_device, d.device = 1, 0
+    return d
+
+
+def gemv_args(m=1, n=64, k=256, bits=4, gs=128, sym=False):
+    per = 32 // bits
+    x = torch.zeros(m, k, dtype=torch.float16)
+    qw = torch.zeros(n, k // per, dtype=torch.int32)
+    sc = torch.zeros(n, k // gs, dtype=torch.float16)
+    ze = None if sym else torch.zeros(n, k // gs, dtype=torch.float16)
+    return x, qw, sc, ze
+
+
+def check_gemv(x, qw, sc, ze, bits=4, gs=128, sym=False):
+    lib = _native.capi()
+    st = lib.dq_check_gemv(x, qw, sc, ze, bits, gs, int(sym))
+    return st, lib.dq_last_error().decode()
+
+
+def test_check_gemv_accepts_valid():
+    x, qw, sc, ze = gemv_args()
+    assert check_gemv(dev(x), dev(qw), dev(sc), dev(ze)) == (0, "")
+    x, qw, sc, ze = gemv_args(m=8, bits=2, gs=64, sym=True)
+    assert check_gemv(dev(x), dev(qw), dev(sc), None, bits=2, gs=64, sym=True) == (0, "")
+
+
+@pytest.mark.parametrize("mutate,status,msg", [
+    (lambda a: a.__setitem__("x", _native.describe(a["x_t"])), 1, "x must be a CUDA tensor"),
+    (lambda a: setattr(a["x"], "dtype", DQ_DTYPE_FLOAT32), 1, "x must be float16"),
+    (lambda a: setattr(a["x"], "contiguous", 0), 1, "x must be contiguous"),
+    (lambda a: setattr(a["x"], "ndim", 3), 1, "x must be 2-D [M, K], got 3-D"),
+    (lambda a: a["x"].sizes.__setitem__(0, 9), 2,
+     "gemv handles 1 <= M <= 8, got M=9; use the dequantize + F.linear fallback"),
+    (lambda a: a["x"].sizes.__setitem__(0, 0), 2,
+     "gemv handles 1 <= M <= 8, got M=0; use the dequantize + F.linear fallback"),
+    (lambda a: setattr(a["x"], "data", a["x"].data + 2), 1, "x must be 16-byte aligned"),
+    (lambda a: a.__setitem__("bits", 3), 1, "bits must be 2, 4 or 8, got 3"),
+    (lambda a: a.__setitem__("gs", 0), 1, "group_size must be positive, got 0"),
+    (lambda a: a.__setitem__("gs", 96), 1, "K=256 is not divisible by group_size=96"),
+    (lambda a: setattr(a["qw"], "is_device", 0), 1, "qweight must be a CUDA tensor"),
+    (lambda a: setattr(a["qw"], "dtype", DQ_DTYPE_FLOAT16), 1, "qweight must be int32"),
+    (lambda a: setattr(a["qw"], "contiguous", 0), 1, "qweight must be contiguous"),
+    (lambda a: setattr(a["qw"], "ndim", 1), 1, "qweight must be 2-D, got 1-D"),
+    (lambda a: a["qw"].sizes.__setitem__(1, 31), 1,
+     "qweight has 31 words per row, which is 248 codes, but K=256"),
+    (lambda a: setattr(a["sc"], "is_device", 0), 1, "scales must be a CUDA tensor"),
+    (lambda a: setattr(a["sc"], "dtype", DQ_DTYPE_FLOAT32), 1, "scales must be float16"),
+    (lambda a: setattr(a["sc"], "contiguous", 0), 1, "scales must be contiguous"),
+    (lambda a: a["sc"].sizes.__setitem__(1, 3), 1, "scales must be [64, 2], got [64, 3]"),
+    (lambda a: setattr(a["sc"], "device", 1), 1, "scales and qweight must be on the same device"),
+    (lambda a: a.__setitem__("ze", None), 1, "symmetric=false requires zeros"),
+    (lambda a: a.__setitem__("sym", True), 1, "symmetric=true takes no zeros"),
+    (lambda a: setattr(a["ze"], "is_device", 0), 1, "zeros must be a CUDA tensor"),
+    (lambda a: setattr(a["ze"], "dtype", DQ_DTYPE_INT32), 1, "zeros must be float16"),
+    (lambda a: setattr(a["ze"], "contiguous", 0), 1, "zeros must be contiguous"),
+    (lambda a: a["ze"].sizes.__setitem__(0, 63), 1, "zeros must have the same shape as scales, got [63, 2]"),
+    (lambda a: setattr(a["ze"], "device", 1), 1, "zeros and qweight must be on the same device"),
+    (lambda a: setattr(a["x"], "device", 1), 1, "x and qweight must be on the same device"),
+])
+def test_check_gemv_messages(mutate, status, msg):
+    x_t, qw_t, sc_t, ze_t = gemv_args()
+    a = {"x_t": x_t, "x": dev(x_t), "qw": dev(qw_t), "sc": dev(sc_t), "ze": dev(ze_t),
+         "bits": 4, "gs": 128, "sym": False}
+    mutate(a)
+    st, text = check_gemv(a["x"], a["qw"], a["sc"], a["ze"], a["bits"], a["gs"], a["sym"])
+    assert (st, text) == (status, msg)
+
+
+def test_check_gemv_int2_group32_rejected():
+    x, qw, sc, _ = gemv_args(bits=2, gs=32, sym=True)
+    st, text = check_gemv(dev(x), dev(qw), dev(sc), None, bits=2, gs=32, sym=True)
+    assert st == 1
+    assert text == ("group_size=32 must be a multiple of 64 (the codes one lane loads per uint4) at 2 bits; "
+                    "this excludes INT2 with group_size 32")
+
+
+def test_check_order_follows_reference():
+    # x is checked before the weight (dequant_gemv.cu:342-354): a bad M wins over bad bits
+    x, qw, sc, ze = gemv_args(m=9)
+    assert check_gemv(dev(x), dev(qw), dev(sc), dev(ze), bits=5)[1].startswith("gemv handles")
+    # bits before group_size before K divisibility (:233-238)
+    assert check_gemv(dev(x[:1]), dev(qw), dev(sc), dev(ze), bits=5, gs=0)[1].startswith("bits must")
+    assert check_gemv(dev(x[:1]), dev(qw), dev(sc), dev(ze), gs=0)[1].startswith("group_size must")
+
+
+def test_check_dequantize_messages():
+    lib = _native.capi()
+    qw = torch.zeros(4, 8, dtype=torch.int32)     # INT4, K = 64
+    sc = torch.zeros(4, 4, dtype=torch.float16)   # g16
+    st = lib.dq_check_dequantize(dev(qw), dev(sc), None, 4, 16, 1, 64)
+    assert (st, lib.dq_last_error()) == (0, b"")
+    sc2 = torch.zeros(4, 16, dtype=torch.float16)  # g4: not a multiple of 8 values per word
+    st = lib.dq_check_dequantize(dev(qw), dev(sc2), None, 4, 4, 1, 64)
+    assert st == 1
+    assert lib.dq_last_error() == b"group_size=4 must be a multiple of 8 values per uint32 word at 4 bits"
+    st = lib.dq_check_dequantize(dev(qw), dev(sc), None, 4, 16, 1, 80)
+    assert lib.dq_last_error() == b"qweight has 8 words per row, which is 64 codes, but K=80"
+
+
+def test_check_unpack_messages():
+    lib = _native.capi()
+    qw = torch.zeros(4, 8, dtype=torch.int32)
+    assert lib.dq_check_unpack(dev(qw), 4, 64) == 0
+    assert lib.dq_check_unpack(dev(qw), 6, 64) == 1
+    assert lib.dq_last_error() == b"bits must be 2, 4 or 8, got 6"
+    assert lib.dq_check_unpack(dev(qw), 2, 64) == 1
+    assert lib.dq_last_error() == b"qweight has 8 words per row, which is 128 codes, but K=64"
+
+
+def test_raw_entry_points_validate_before_any_launch():
+    lib = _native.capi()
+    P = ctypes.c_void_p
+    fake = P(0x1000)  # never dereferenced: every call below fails validation first
+    assert lib.dq_gemv(fake, fake, fake, None, fake, 9, 4, 256, 4, 128, 1, 0, None) == 2
+    assert lib.dq_last_error().startswith(b"gemv handles 1 <= M <= 8, got M=9")
+    assert lib.dq_gemv(P(0x1002), fake, fake, None, fake, 1, 4, 256, 4, 128, 1, 0, None) == 1
+    assert lib.dq_last_error() == b"x must be 16-byte aligned"
+    assert lib.dq_gemv(fake, fake, fake, fake, fake, 1, 4, 256, 4, 128, 1, 0, None) == 1
+    assert lib.dq_last_error() == b"symmetric=true takes no zeros"
+    assert lib.dq_gemv(fake, fake, fake, None, fake, 1, 4, 256, 2, 32, 1, 0, None) == 1
+    assert lib.dq_last_error().startswith(b"group_size=32 must be a multiple of 64")
+    assert lib.dq_gemv(fake, P(0x1004), fake, None, fake, 1, 4, 256, 4, 128, 1, 0, None) == 1
+    assert lib.dq_last_error() == b"qweight must be 16-byte aligned"
+    assert lib.dq_gemv(None, fake, fake, None, fake, 1, 4, 256, 4, 128, 1, 0, None) == 1
+    assert lib.dq_dequantize(fake, fake, None, fake, 4, 256, 8, 2, 1, 0, None) == 1
+    assert lib.dq_last_error() == b"group_size=2 must be a multiple of 4 values per uint32 word at 8 bits"
+    assert lib.dq_unpack(fake, P(0x1008), 4, 256, 4, 0, None) == 1
+    assert lib.dq_last_error() == b"out must be 16-byte aligned"
+    assert lib.dq_add_one(fake, fake, -1, None) == 1
+    # empty problems are a no-op success without touching the GPU
+    assert lib.dq_gemv(fake, fake, fake, None, fake, 1, 0, 256, 4, 128, 1, 0, None) == 0
+    assert lib.dq_add_one(None, None, 0, None) == 0
+
+
+def test_torch_binding_rejects_cpu_tensors_with_reference_messages():
+    ext = _native.ext()
+    x, qw, sc, ze = gemv_args()
+    with pytest.raises(RuntimeError, match="^x must be a CUDA tensor$"):
+        ext.gemv(x, qw, sc, ze, 4, 128, False, False)
+    with pytest.raises(RuntimeError, match="^qweight must be a CUDA tensor$"):
+        ext.dequantize(qw, sc, ze, 4, 128, False, False, 256)
+    with pytest.raises(RuntimeError, match="^x must be a CUDA tensor$"):
+        ext.add_one(torch.ones(4))
+    # keyword names of kernels/bindings.cpp:6-16
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ext.gemv(x=x, qweight=qw, scales=sc, zeros=ze, bits=4, group_size=128, symmetric=False,
+                 interleaved=False)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ext.dequantize(qweight=qw, scales=sc, zeros=ze, bits=4, group_size=128, symmetric=False,
+                       interleaved=False, K=256)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ext.unpack(qweight=qw, bits=4, interleaved=False, K=256)

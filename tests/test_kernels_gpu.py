@@ -1,0 +1,399 @@
+"""Parity of the HIP kernels with the CPU oracle (MI355X only).
+
+Restates scripts/test_dequant_kernel.py of the reference (tests 1-5, :56-252)
+and extends it to the benchmark configurations and edge shapes:
+
+  unpack       bit-exact with oracle.packer_ref.unpack and the reference's
+               golden codes
+  dequantize   bit-exact (torch.equal) with the oracle and the golden fp16
+               weights, every bits x layout x symmetry x group, gauss + skew
+  gemv         two tolerances, both written here:
+                 * the reference's elementwise fp32-accumulation criterion
+                   |y - ref| <= 2^-11 |ref| + 2^-20 |W|@|x| against the fp64
+                   product of exact_weight (test_dequant_kernel.py:112-122);
+                 * the north star's rel-L2 <= 1e-3 against fp32
+                   dequantize-then-matmul.
+Weights come from seeded numpy generators; the packed tensors are made by the
+product packer on the GPU and read back, so the oracle and the kernel consume
+the same bytes.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import packer_ref as P
+from tests._helpers import (GOLDEN_CASES, activations, gauss_weight, golden, golden_tag,
+                            outlier_weight, skew_weight)
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_TOL = 1e-3   # north star: GEMV within rel-L2 <= 1e-3 of fp32 dequantize-then-matmul
+
+
+# ------------------------------------------------------------------ helpers
+def ext():
+    from dequant_project_amd import _native
+    return _native.ext()
+
+
+def to_gpu(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def pack_on_gpu(torch, w16, bits, gs, sym, layout):
+    """Product packer on the GPU; returns (pw, numpy copies for the oracle)."""
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    pw = quantize_tensor(to_gpu(torch, w16), QuantConfig(bits, gs, sym, layout))
+    qw = pw.qweight.cpu().numpy()
+    sc = pw.scales.cpu().numpy()
+    ze = None if pw.zeros is None else pw.zeros.cpu().numpy()
+    return pw, qw, sc, ze
+
+
+def ext_args(pw):
+    k = pw.shape[1]
+    cfg = pw.config
+    return (pw.qweight, pw.scales, pw.zeros, cfg.bits, cfg.effective_group_size(k), cfg.symmetric,
+            cfg.layout == "interleaved")
+
+
+class OracleCase:
+    """Oracle-side view of one packed weight: exact_weight in fp64 (and its
+    absolute value) for the criterion, packer.dequantize's fp16 weight for the
+    rel-L2 check. rows: optional sample of output rows."""
+
+    def __init__(self, pw, qw, sc, ze, rows=None):
+        n, k = pw.shape
+        self.cfg = P.Config(pw.config.bits, pw.config.group_size, pw.config.symmetric, pw.config.layout)
+        if rows is not None:
+            qw, sc = qw[rows], sc[rows]
+            ze = None if ze is None else ze[rows]
+            n = len(rows)
+        self.rows = rows
+        self.w64 = P.exact_weight(qw, sc, ze, self.cfg, (n, k)).astype(np.float64)
+        self.absw64 = np.abs(self.w64)
+        self.deq32 = P.dequantize(qw, sc, ze, self.cfg, (n, k)).astype(np.float32)
+
+    def check(self, y, x16, label):
+        if self.rows is not None:
+            y = y[:, self.rows]
+        x64 = x16.astype(np.float64)
+        ref = x64 @ self.w64.T
+        absref = np.abs(x64) @ self.absw64.T
+        ok, worst = P.gemv_criterion(y, ref, absref)
+        rl2 = P.rel_l2(y, x16.astype(np.float32) @ self.deq32.T)
+        print(f"{label}: worst={worst:.3f}x tol rel_l2={rl2:.2e}", flush=True)
+        assert ok, f"{label}: elementwise criterion violated, worst {worst:.3f}x tol"
+        assert rl2 <= REL_L2_TOL, f"{label}: rel-L2 {rl2:.3e} > {REL_L2_TOL}"
+
+
+def run_gemv(torch, pw, x16):
+    return ext().gemv(to_gpu(torch, x16), *ext_args(pw)).cpu().numpy()
+
+
+def check_gemv(torch, pw, qw, sc, ze, x16s, label, rows=None):
+    """Run the fused GEMV for each x in x16s and apply both tolerances."""
+    case = OracleCase(pw, qw, sc, ze, rows)
+    for x16 in x16s:
+        case.check(run_gemv(torch, pw, x16), x16, f"{label} M={x16.shape[0]}")
+
+
+# --------------------------------------------------------- 1. extension loads
+def test_extension_loads(torch_gpu):
+    torch = torch_gpu
+    out = ext().add_one(torch.ones(4, device="cuda"))
+    assert torch.equal(out, torch.full((4,), 2.0, device="cuda"))
+    big = torch.arange(1 << 20, dtype=torch.float32, device="cuda")
+    assert torch.equal(ext().add_one(big), big + 1)
+
+
+# ------------------------------------------------------------------- unpack
+@pytest.mark.parametrize("bits", (2, 4, 8))
+@pytest.mark.parametrize("layout", ("sequential", "interleaved"))
+def test_unpack_bit_exact(torch_gpu, bits, layout):
+    torch = torch_gpu
+    cfg = P.Config(bits, None, True, layout)
+    for n, k in [(1, 32 // bits), (37, 256), (1024, 3072)]:
+        words = np.random.Generator(np.random.PCG64(n * k + bits)).integers(
+            0, 2 ** 32, (n, k // cfg.per_pack), dtype=np.uint64).astype(np.uint32).view(np.int32)
+        got = ext().unpack(to_gpu(torch, words), bits, layout == "interleaved", k).cpu().numpy()
+        assert np.array_equal(got, P.unpack(words, cfg, k)), (n, k)
+
+
+@pytest.mark.parametrize("bits,gs,sym,layout", GOLDEN_CASES, ids=[golden_tag(*c) for c in GOLDEN_CASES])
+def test_unpack_and_dequantize_match_reference_golden(torch_gpu, bits, gs, sym, layout):
+    torch = torch_gpu
+    g = golden()
+    t = golden_tag(bits, gs, sym, layout)
+    n, k = g["w16"].shape
+    qw = to_gpu(torch, g[t + "/qweight"])
+    codes = ext().unpack(qw, bits, layout == "interleaved", k).cpu().numpy()
+    assert np.array_equal(codes, g[t + "/codes"])
+    sc = to_gpu(torch, g[t + "/scales"].view(np.float16))
+    ze = None if sym else to_gpu(torch, g[t + "/zeros"].view(np.float16))
+    deq = ext().dequantize(qw, sc, ze, bits, k if gs is None else gs, sym, layout == "interleaved", k)
+    assert np.array_equal(deq.cpu().numpy().view(np.uint16), g[t + "/deq"])
+
+
+# --------------------------------------------------------------- dequantize
+@pytest.mark.parametrize("bits", (2, 4, 8))
+@pytest.mark.parametrize("layout", ("sequential", "interleaved"))
+def test_dequantize_bit_exact(torch_gpu, bits, layout):
+    """scripts/test_dequant_kernel.py:63-89: torch.equal over sym x group x data."""
+    torch = torch_gpu
+    n, k = 1024, 3072
+    gauss = gauss_weight(n, k, seed=100)
+    skew = skew_weight(n, k, seed=101)
+    for sym in (True, False):
+        for gs in (32, 64, 128, 256, None):
+            for tag, w in ([("gauss", gauss)] if sym else [("gauss", gauss), ("skew", skew)]):
+                pw, qw, sc, ze = pack_on_gpu(torch, w, bits, gs, sym, layout)
+                got = ext().dequantize(*ext_args(pw), k).cpu().numpy()
+                want = P.dequantize(qw, sc, ze, P.Config(bits, gs, sym, layout), (n, k))
+                bad = int((got.view(np.uint16) != want.view(np.uint16)).sum())
+                assert bad == 0, f"{bits}-bit {layout} sym={sym} g{gs} {tag}: {bad} values differ"
+
+
+def test_gpu_packer_matches_cpu_packer(torch_gpu):
+    """The product packer gives the same bytes on the GPU as on the CPU."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    w = torch.from_numpy(outlier_weight(512, 4096, seed=7))
+    for args in [(4, 128, False, "sequential"), (2, 64, False, "interleaved"), (8, None, True, "sequential"),
+                 (4, 32, True, "interleaved")]:
+        a = quantize_tensor(w, QuantConfig(*args))
+        b = quantize_tensor(w.cuda(), QuantConfig(*args))
+        assert torch.equal(a.qweight, b.qweight.cpu()), args
+        assert torch.equal(a.scales, b.scales.cpu()), args
+        assert (a.zeros is None) == (b.zeros is None)
+        if a.zeros is not None:
+            assert torch.equal(a.zeros, b.zeros.cpu()), args
+
+
+# --------------------------------------------------------------------- gemv
+GEMV_FORMATS = [  # scripts/test_dequant_kernel.py:137-145, plus INT2 and asym INT8
+    (4, 128, True, "sequential"), (4, 128, False, "sequential"),
+    (4, 128, True, "interleaved"), (4, 128, False, "interleaved"),
+    (8, 128, True, "sequential"), (8, 128, True, "interleaved"),
+    (4, None, True, "sequential"),
+    (2, 64, True, "sequential"), (2, 64, False, "interleaved"), (2, 128, False, "sequential"),
+    (8, None, False, "interleaved"), (8, 16, False, "sequential"), (4, 32, False, "interleaved"),
+]
+GEMV_SHAPES = [(3072, 3072), (1024, 3072), (8192, 3072), (3072, 8192)]
+
+
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+def test_gemv_reference_suite(torch_gpu, n, k):
+    """scripts/test_dequant_kernel.py:149-172 (M in {1,2,3,8}) over more formats."""
+    torch = torch_gpu
+    w16 = gauss_weight(n, k, seed=n + k)
+    for fmt in GEMV_FORMATS:
+        pw, qw, sc, ze = pack_on_gpu(torch, w16, *fmt)
+        check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=m) for m in (1, 2, 3, 8)], f"[{n},{k}] {fmt}")
+
+
+@pytest.mark.parametrize("m", range(1, 9))
+def test_gemv_every_m(torch_gpu, m):
+    torch = torch_gpu
+    n, k = 777, 2048
+    for fmt in [(4, 128, False, "sequential"), (2, 64, False, "sequential"), (8, None, True, "interleaved")]:
+        pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(n, k, seed=5), *fmt)
+        check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=10 + m)], f"{fmt}")
+
+
+@pytest.mark.parametrize("n,k,fmt", [
+    (1, 128, (4, 128, False, "sequential")),      # a single row
+    (3, 64, (2, 64, True, "interleaved")),        # one chunk per row
+    (17, 16, (8, 16, False, "sequential")),       # K = one 16-byte chunk at INT8
+    (5, 4160, (2, 64, False, "sequential")),      # 65 chunks: one lane takes two
+    (19, 4096 + 64 * 32, (4, 64, True, "interleaved")),
+    (65, 11008, (2, 64, False, "sequential")),    # 172 chunks (config C3's K)
+    (130, 28672, (2, 64, False, "interleaved")),  # C5 down_proj K
+    (31, 8192, (8, None, True, "sequential")),    # C5 lm_head K
+])
+def test_gemv_edge_shapes(torch_gpu, n, k, fmt):
+    torch = torch_gpu
+    pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(n, k, seed=n * 3 + k), *fmt)
+    check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=m + 1) for m in (1, 4, 8)], f"[{n},{k}] {fmt}")
+
+
+def test_gemv_skewed_weights_negative_zero_points(torch_gpu):
+    torch = torch_gpu
+    n, k = 512, 4096
+    for fmt in [(4, 128, False, "sequential"), (2, 64, False, "interleaved"), (8, 128, False, "sequential"),
+                (8, None, False, "sequential")]:
+        pw, qw, sc, ze = pack_on_gpu(torch, skew_weight(n, k, seed=21), *fmt)
+        assert (ze.astype(np.float32) < 0).any()
+        check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=22) for m in (1, 8)], f"skew {fmt}")
+
+
+# ------------------------------------------------------- benchmark configs
+def test_config_c1_int4_asym_g128(torch_gpu):
+    torch = torch_gpu
+    pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(4096, 4096, seed=1), 4, 128, False, "sequential")
+    check_gemv(torch, pw, qw, sc, ze, [activations(1, 4096, seed=1)], "C1")
+
+
+def test_config_c2_int8_per_channel(torch_gpu):
+    torch = torch_gpu
+    pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(11008, 4096, seed=2), 8, None, True, "sequential")
+    check_gemv(torch, pw, qw, sc, ze, [activations(m, 4096, seed=2 + m) for m in (1, 4)], "C2")
+
+
+def test_config_c3_int2_asym_g64_outliers(torch_gpu):
+    torch = torch_gpu
+    pw, qw, sc, ze = pack_on_gpu(torch, outlier_weight(4096, 11008, seed=3), 2, 64, False, "sequential")
+    check_gemv(torch, pw, qw, sc, ze, [activations(1, 11008, seed=3)], "C3")
+
+
+@pytest.mark.parametrize("name,n,k,fmt", [
+    ("C4 q/o", 4096, 4096, (4, 128, False, "sequential")),
+    ("C4 k/v", 1024, 4096, (4, 128, False, "sequential")),
+    ("C4 gate/up", 14336, 4096, (4, 128, False, "sequential")),
+    ("C4 down", 4096, 14336, (4, 128, False, "sequential")),
+    ("C5 q/o", 8192, 8192, (4, 128, False, "sequential")),
+    ("C5 gate/up", 28672, 8192, (2, 64, False, "sequential")),
+    ("C5 down", 8192, 28672, (2, 64, False, "sequential")),
+])
+def test_config_layer_shapes(torch_gpu, name, n, k, fmt):
+    """Llama-3-8B / 70B projection shapes; M sweep of C4; rows sampled for the fp64 reference."""
+    torch = torch_gpu
+    pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(n, k, seed=n ^ k), *fmt)
+    rows = np.sort(np.random.Generator(np.random.PCG64(n)).choice(n, min(n, 1024), replace=False))
+    check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=m) for m in (1, 2, 4, 8)], name, rows=rows)
+
+
+def test_config_c5_lm_head_int8_sampled(torch_gpu):
+    torch = torch_gpu
+    n, k = 128256, 8192
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    w = torch.randn(n, k, generator=torch.Generator(device="cuda").manual_seed(5), device="cuda",
+                    dtype=torch.float16) * 0.02
+    pw = quantize_tensor(w, QuantConfig(8, None, True))
+    del w
+    rows = np.sort(np.random.Generator(np.random.PCG64(9)).choice(n, 512, replace=False))
+    qw = pw.qweight[torch.from_numpy(rows).cuda()].cpu().numpy()
+    sc = pw.scales[torch.from_numpy(rows).cuda()].cpu().numpy()
+    x16 = activations(1, k, seed=12)
+    y = ext().gemv(to_gpu(torch, x16), *ext_args(pw)).cpu().numpy()[:, rows]
+    cfg = P.Config(8, None, True)
+    ew = P.exact_weight(qw, sc, None, cfg, (len(rows), k))
+    ref, absref = P.gemv_reference(x16, ew)
+    ok, worst = P.gemv_criterion(y, ref, absref)
+    assert ok, worst
+    assert P.rel_l2(y, x16.astype(np.float32) @ P.dequantize(qw, sc, None, cfg, (len(rows), k))
+                    .astype(np.float32).T) <= REL_L2_TOL
+
+
+# ----------------------------------------------------------- errors (3b)
+def test_excluded_formats_raise(torch_gpu):
+    """scripts/test_dequant_kernel.py:174-191."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    pw = quantize_tensor(torch.randn(64, 256, device="cuda", dtype=torch.float16), QuantConfig(2, 32, True))
+    with pytest.raises(RuntimeError, match="this excludes INT2 with group_size 32"):
+        ext().gemv(torch.randn(1, 256, device="cuda", dtype=torch.float16), *ext_args(pw))
+    pw = quantize_tensor(torch.randn(64, 256, device="cuda", dtype=torch.float16), QuantConfig(4, 128, True))
+    with pytest.raises(RuntimeError, match=r"^gemv handles 1 <= M <= 8, got M=9"):
+        ext().gemv(torch.randn(9, 256, device="cuda", dtype=torch.float16), *ext_args(pw))
+    buf = torch.randn(258, device="cuda", dtype=torch.float16)
+    x_misaligned = buf[1:257].view(1, 256)          # contiguous, 2 bytes past an aligned address
+    with pytest.raises(RuntimeError, match="^x must be 16-byte aligned$"):
+        ext().gemv(x_misaligned, *ext_args(pw))
+
+
+# -------------------------------------------------- 4. negative control
+def test_negative_control(torch_gpu):
+    """scripts/test_dequant_kernel.py:194-217: one flipped bit fails only [0, 0]."""
+    torch = torch_gpu
+    n, k = 3072, 3072
+    pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(n, k, seed=0), 4, 128, True, "sequential")
+    x16 = activations(1, k, seed=0)
+    x16[0, 0] = np.float16(1.0)
+    cfg = P.Config(4, 128, True, "sequential")
+    ref, absref = P.gemv_reference(x16, P.exact_weight(qw, sc, ze, cfg, (n, k)))
+    bad = pw.qweight.clone()
+    bad[0, 0] ^= 1
+    y = ext().gemv(to_gpu(torch, x16), bad, pw.scales, None, 4, 128, True, False).cpu().numpy()
+    tol = 2.0 ** -11 * np.abs(ref) + 2.0 ** -20 * absref
+    over = np.abs(y.astype(np.float64) - ref) > tol
+    assert over[0, 0], "flipped bit not detected"
+    assert int(over.sum()) == 1, f"{int(over.sum())} elements over tolerance"
+
+
+# ---------------------------------------------------- 5. graph capture
+def test_graph_capture_replays_live_input(torch_gpu):
+    """scripts/test_dequant_kernel.py:220-252."""
+    torch = torch_gpu
+    n, k = 3072, 3072
+    pw, *_ = pack_on_gpu(torch, gauss_weight(n, k, seed=0), 4, 128, False, "sequential")
+    args = ext_args(pw)
+    x = to_gpu(torch, activations(1, k, seed=1))
+    x2 = to_gpu(torch, activations(1, k, seed=2))
+    eager1 = ext().gemv(x, *args).clone()
+    eager2 = ext().gemv(x2, *args).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            ext().gemv(x, *args)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = ext().gemv(x, *args)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager1)
+    x.copy_(x2)
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, eager2)
+
+
+def test_results_are_deterministic(torch_gpu):
+    torch = torch_gpu
+    pw, *_ = pack_on_gpu(torch, gauss_weight(4096, 4096, seed=8), 2, 64, False, "sequential")
+    x = to_gpu(torch, activations(4, 4096, seed=8))
+    y0 = ext().gemv(x, *ext_args(pw))
+    for _ in range(5):
+        assert torch.equal(ext().gemv(x, *ext_args(pw)), y0)
+
+
+# ------------------------------------------------------- direct C ABI
+def test_c_abi_matches_extension(torch_gpu):
+    """Calls through include/dequant_hip.h with raw device pointers (ctypes)."""
+    torch = torch_gpu
+    from dequant_project_amd import _native
+
+    lib = _native.capi()
+    stream = torch.cuda.current_stream().cuda_stream
+    n, k = 2048, 4096
+    for fmt in [(4, 128, False, "sequential"), (2, 64, True, "interleaved"), (8, None, True, "sequential")]:
+        pw, *_ = pack_on_gpu(torch, gauss_weight(n, k, seed=31), *fmt)
+        bits, gs, sym, inter = fmt[0], fmt[1] or k, fmt[2], fmt[3] == "interleaved"
+        for m in (1, 5):
+            x = to_gpu(torch, activations(m, k, seed=m))
+            y = torch.empty(m, n, dtype=torch.float16, device="cuda")
+            st = lib.dq_gemv(x.data_ptr(), pw.qweight.data_ptr(), pw.scales.data_ptr(),
+                             None if sym else pw.zeros.data_ptr(), y.data_ptr(), m, n, k, bits, gs,
+                             int(sym), int(inter), stream)
+            assert st == 0, lib.dq_last_error()
+            assert torch.equal(y, ext().gemv(x, *ext_args(pw)))
+        out = torch.empty(n, k, dtype=torch.float16, device="cuda")
+        st = lib.dq_dequantize(pw.qweight.data_ptr(), pw.scales.data_ptr(),
+                               None if sym else pw.zeros.data_ptr(), out.data_ptr(), n, k, bits, gs, int(sym),
+                               int(inter), stream)
+        assert st == 0 and torch.equal(out, ext().dequantize(*ext_args(pw), k))
+        codes = torch.empty(n, k, dtype=torch.int32, device="cuda")
+        st = lib.dq_unpack(pw.qweight.data_ptr(), codes.data_ptr(), n, k, bits, int(inter), stream)
+        assert st == 0 and torch.equal(codes, ext().unpack(pw.qweight, bits, inter, k))
+    a = torch.arange(1000, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    assert lib.dq_add_one(a.data_ptr(), b.data_ptr(), 1000, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(b, a + 1)
