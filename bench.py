@@ -1,0 +1,418 @@
+#!/usr/bin/env python3
+"""Fused dequant-GEMV benchmark on one MI355X.
+
+Workload: the Llama-3-8B decoder linear set --
+32 layers x {q 4096->4096, k 4096->1024, v 4096->1024, o 4096->4096,
+gate 4096->14336, up 4096->14336, down 14336->4096} -- quantized INT4
+asymmetric, group 128, at batch M = 1. Weights are fp16 N(0, 0.02) from a
+seeded generator, quantized on the GPU by the engine's packer (3.71 GB packed,
+well past the 256 MB Infinity Cache, so every step streams from HBM);
+activations are fp16 N(0, 1). Everything is resident in HBM before timing.
+
+One step = one decode pass of the hot path over the whole stack, captured in a
+HIP graph. Per layer it launches what a decoder launches, given the data
+dependencies of a Llama layer: q|k|v grouped (same input), o, gate|up grouped
+(same input), down -- 4 launches per layer, 128 per step. Also measured and
+reported: the same step as 7 per-linear launches per layer (the QuantLinear
+drop-in path), and the rotating-copy single-config runs of C1/C2/C3.
+
+Printed: ONE JSON line on stdout (progress goes to stderr).
+  value       whole-step algorithmic bytes / step time, GB/s (the
+              byte_model accounting: packed weights + scales + zeros + x + y)
+  roofline    the dominant kernel instance: algorithmic bytes per launch /
+              its mean kernel duration (timed with HIP events recorded by the
+              kernel dispatch itself, hipExtLaunchKernelGGL, on the launch
+              stream), against the 8 TB/s HBM3E peak
+  cpu_baseline  the reference's CPU torch path (oracle/cpu_path.py) on one
+              layer of the same stack, on this host's cores
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fused dequant-GEMV HBM GB/s (% of MI355X peak) + µs/layer, INT2/4/8, batch 1"
+PEAK_GBS = 8000.0
+LAYERS = 32
+HIDDEN, KV, INTER = 4096, 1024, 14336
+PROJS = [("q_proj", HIDDEN, HIDDEN), ("k_proj", KV, HIDDEN), ("v_proj", KV, HIDDEN),
+         ("o_proj", HIDDEN, HIDDEN), ("gate_proj", INTER, HIDDEN), ("up_proj", INTER, HIDDEN),
+         ("down_proj", HIDDEN, INTER)]
+GROUPS = [("qkv", ("q_proj", "k_proj", "v_proj")), ("o", ("o_proj",)),
+          ("gate_up", ("gate_proj", "up_proj")), ("down", ("down_proj",))]
+MALL_BYTES = 256 * 2 ** 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def summarize(samples):
+    s = sorted(samples)
+    n = len(s)
+    return {"median": statistics.median(s), "p25": s[n // 4], "p75": s[(3 * n) // 4],
+            "min": s[0], "max": s[-1], "n": n}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=LAYERS, help=argparse.SUPPRESS)
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C1/C2/C3 single-config runs")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 1 GiB device copy (rocprof FETCH_SIZE/WRITE_SIZE calibration)")
+    return ap.parse_args()
+
+
+class Engine:
+    """The engine's entry points used here: the torch extension for launches,
+    the C ABI for the launch plan and the kernel-timing hook."""
+
+    def __init__(self, torch):
+        from dequant_project_amd import _native
+
+        self.torch = torch
+        self.ext = _native.ext()
+        self.capi = _native.capi()
+        self.native = _native
+
+    def gemv_group(self, xs, pws):
+        cfg = pws[0].config
+        if len(pws) == 1:
+            pw = pws[0]
+            return [self.ext.gemv(xs[0], pw.qweight, pw.scales, pw.zeros, cfg.bits,
+                                  cfg.effective_group_size(pw.shape[1]), cfg.symmetric,
+                                  cfg.layout == "interleaved")]
+        return self.ext.gemv_batched(xs, [p.qweight for p in pws], [p.scales for p in pws],
+                                     [p.zeros for p in pws], cfg.bits,
+                                     [p.config.effective_group_size(p.shape[1]) for p in pws], cfg.symmetric,
+                                     cfg.layout == "interleaved")
+
+    def kernel_name(self, xs, pws):
+        """Kernel instance a launch of these problems uses (dq_gemv_plan)."""
+        n = len(pws)
+        arr = (self.native.DqGemvProblem * n)()
+        for i, (x, p) in enumerate(zip(xs, pws)):
+            arr[i].N, arr[i].K = p.shape
+            arr[i].group_size = p.config.effective_group_size(p.shape[1])
+        wk, rows = (ctypes.c_int * n)(), ctypes.c_int()
+        cfg = pws[0].config
+        m = xs[0].shape[0]
+        st = self.capi.dq_gemv_plan(arr, n, m, cfg.bits, wk, ctypes.byref(rows))
+        self.native.check(st)
+        mt = 1 if m == 1 else (2 if m == 2 else (4 if m <= 4 else 8))
+        return (f"gemv_batched_kernel<{cfg.bits}, {str(cfg.symmetric).lower()}, "
+                f"{str(cfg.layout == 'interleaved').lower()}, {mt}, {rows.value}, 2>"), tuple(wk)
+
+    def timed_launch(self, xs, pws):
+        """One eager launch whose kernel is bracketed by dispatch-recorded events; returns ms."""
+        torch = self.torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        e1.record()  # creates both events
+        self.native.check(self.capi.dq_set_launch_events(e0.cuda_event, e1.cuda_event))
+        self.gemv_group(xs, pws)
+        e1.synchronize()
+        return e0.elapsed_time(e1)
+
+
+def build_stack(torch, layers, seed=20251201):
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    cfg = QuantConfig(4, 128, False, "sequential")
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    stack = []
+    for _ in range(layers):
+        layer = {}
+        for name, n, k in PROJS:
+            w = torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02
+            layer[name] = quantize_tensor(w, cfg)
+            del w
+        stack.append(layer)
+    xs = []
+    for _ in range(layers):
+        xs.append({"qkv": torch.randn(1, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+                   "o": torch.randn(1, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+                   "gate_up": torch.randn(1, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+                   "down": torch.randn(1, INTER, generator=gen, device="cuda", dtype=torch.float16)})
+    return cfg, stack, xs
+
+
+def step_launches(stack, xs, mode):
+    """[(role, [x...], [pw...])] of one step."""
+    out = []
+    for layer, x in zip(stack, xs):
+        for role, names in GROUPS:
+            if mode == "grouped":
+                out.append((role, [x[role]] * len(names), [layer[n] for n in names]))
+            else:
+                for n in names:
+                    out.append((role, [x[role]], [layer[n]]))
+    return out
+
+
+def launch_bytes(xs, pws):
+    from dequant_project_amd import byte_model as bm
+
+    total = 0
+    for x, p in zip(xs, pws):
+        c = p.config
+        total += bm.gemv_call_bytes(p.shape[0], p.shape[1], c.bits, c.group_size, c.symmetric, x.shape[0])
+    return total
+
+
+def capture(torch, fn):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def time_graph(torch, graph, steps, warmup):
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record()
+    for i in range(steps):
+        graph.replay()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    return evs[0].elapsed_time(evs[-1]) / steps, per
+
+
+def run_mode(torch, eng, stack, xs, mode, steps, warmup):
+    launches = step_launches(stack, xs, mode)
+    step_bytes = sum(launch_bytes(x, p) for _, x, p in launches)
+
+    def fn():
+        for _, x, p in launches:
+            eng.gemv_group(x, p)
+
+    graph = capture(torch, fn)
+    ms, per = time_graph(torch, graph, steps, warmup)
+    del graph
+    return launches, step_bytes, ms, per
+
+
+def kernel_stats(torch, eng, launches, reps=3):
+    """Per kernel instance: launches per step, bytes per launch, mean duration (events)."""
+    stats = {}
+    for _, x, p in launches:  # warm
+        eng.gemv_group(x, p)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        for role, x, p in launches:
+            name, wk = eng.kernel_name(x, p)
+            ms = eng.timed_launch(x, p)
+            s = stats.setdefault(name, {"launch_ms": [], "bytes": [], "roles": set(), "wk": set()})
+            s["launch_ms"].append(ms)
+            s["bytes"].append(launch_bytes(x, p))
+            s["roles"].add(role)
+            s["wk"].add(wk)
+    out = {}
+    for name, s in stats.items():
+        mean_ms = sum(s["launch_ms"]) / len(s["launch_ms"])
+        mean_bytes = sum(s["bytes"]) / len(s["bytes"])
+        out[name] = {"launches_per_step": len(s["launch_ms"]) // reps, "mean_us": mean_ms * 1e3,
+                     "bytes_per_launch": mean_bytes, "gbs": mean_bytes / (mean_ms * 1e-3) / 1e9,
+                     "roles": sorted(s["roles"]), "waves_per_tile": sorted(s["wk"]),
+                     "time_share": sum(s["launch_ms"])}
+    total = sum(v["time_share"] for v in out.values())
+    for v in out.values():
+        v["time_share"] = v["time_share"] / total
+    return out
+
+
+def cpu_baseline(torch, stack):
+    """The reference's CPU torch path (unpack -> dequantize -> fp32 F.linear) on layer 0."""
+    from oracle import cpu_path
+
+    layer = stack[0]
+    cpu = {n: (p.qweight.cpu(), p.scales.cpu(), p.zeros.cpu(), p.config, p.shape) for n, p in layer.items()}
+    gen = torch.Generator().manual_seed(3)
+    xs = {n: torch.randn(1, shape[1], generator=gen, dtype=torch.float16) for n, (*_, shape) in cpu.items()}
+    layer_bytes = sum(launch_bytes([xs[n]], [p]) for n, p in layer.items())
+
+    def one_layer(matmul_only=None):
+        for n, (qw, sc, ze, c, shape) in cpu.items():
+            if matmul_only is None:
+                cpu_path.gemv(xs[n], qw, sc, ze, c.bits, c.effective_group_size(shape[1]), c.symmetric,
+                              c.layout == "interleaved")
+            else:
+                torch.nn.functional.linear(xs[n].float(), matmul_only[n])
+
+    threads = torch.get_num_threads()
+    t0 = time.perf_counter()
+    one_layer()  # warm-up
+    warm = time.perf_counter() - t0
+    reps = max(3, min(20, int(15.0 / max(warm, 1e-3))))
+    samples = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        one_layer()
+        samples.append(time.perf_counter() - t0)
+    med = statistics.median(samples)
+    weights = {n: cpu_path.dequantize(qw, sc, ze, c.bits, c.effective_group_size(shape[1]), c.symmetric,
+                                      c.layout == "interleaved", shape[1]).float()
+               for n, (qw, sc, ze, c, shape) in cpu.items()}
+    mm = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        one_layer(weights)
+        mm.append(time.perf_counter() - t0)
+    return {"value": layer_bytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"one Llama-3-8B layer (7 linears, {layer_bytes / 1e6:.1f} MB packed INT4 g128 asym, M=1) "
+                       f"of the benchmark stack, unpack -> dequantize -> fp32 F.linear "
+                       f"(oracle/cpu_path.py), median of {reps} after 1 warm-up"),
+            "us_per_layer": med * 1e6, "matmul_only_us_per_layer": statistics.median(mm) * 1e6,
+            "os_cpu_count": os.cpu_count()}
+
+
+def single_config(torch, eng, name, n, k, cfg, m, reps=10):
+    """The reference's rotating-copy microbenchmark for one shape (working set
+    >= 8 x the 256 MB Infinity Cache): per-call graph time and kernel time."""
+    from dequant_project_amd.packer import quantize_tensor
+
+    gen = torch.Generator(device="cuda").manual_seed(n * 7 + k)
+    first = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02, cfg)
+    copies = max(4, math.ceil(8 * MALL_BYTES / first.nbytes))
+    pws = [first] + [quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02,
+                                     cfg) for _ in range(copies - 1)]
+    x = torch.randn(m, k, generator=gen, device="cuda", dtype=torch.float16)
+
+    def fn():
+        for p in pws:
+            eng.gemv_group([x], [p])
+
+    graph = capture(torch, fn)
+    ms, per = time_graph(torch, graph, reps, 2)
+    kms = [eng.timed_launch([x], [p]) for p in pws[:min(copies, 64)]]
+    b = launch_bytes([x], [first])
+    kernel_us = statistics.median(kms) * 1e3
+    res = {"shape": [n, k], "M": m, "format": f"INT{cfg.bits} g{cfg.group_size or 'pc'} "
+           f"{'sym' if cfg.symmetric else 'asym'}", "copies": copies, "bytes_per_call": b,
+           "us_per_call_graph": statistics.median(per) * 1e3 / copies,
+           "kernel_us": kernel_us, "kernel_gbs": b / (kernel_us * 1e-6) / 1e9,
+           "kernel_pct_peak": 100 * b / (kernel_us * 1e-6) / 1e9 / PEAK_GBS}
+    res["graph_gbs"] = b / (res["us_per_call_graph"] * 1e-6) / 1e9
+    del graph, pws, first
+    torch.cuda.empty_cache()
+    return name, res
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the sharding design is described in DESIGN.md", file=sys.stderr)
+        return 2
+    import torch
+
+    from dequant_project_amd.packer import QuantConfig
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    eng = Engine(torch)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    log(f"device: {torch.cuda.get_device_name(0)}  torch {torch.__version__}")
+
+    if args.calibrate_copy:
+        src = torch.empty(2 ** 28, dtype=torch.int32, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 1 GiB read + 1 GiB write, 3 times")
+        del src, dst
+
+    t0 = time.perf_counter()
+    cfg, stack, xs = build_stack(torch, args.layers)
+    torch.cuda.synchronize()
+    log(f"built {args.layers}-layer INT4 stack in {time.perf_counter() - t0:.1f}s")
+
+    modes = {}
+    for mode in ("grouped", "per_linear"):
+        launches, step_bytes, ms, per = run_mode(torch, eng, stack, xs, mode, args.steps, args.warmup)
+        st = summarize(per)
+        modes[mode] = {"launches_per_step": len(launches), "bytes_per_step": step_bytes, "ms_per_step": ms,
+                       "step_ms": st, "gbs": step_bytes / (ms * 1e-3) / 1e9,
+                       "us_per_layer": ms * 1e3 / args.layers,
+                       "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS}
+        log(f"mode {mode}: {ms:.3f} ms/step  {modes[mode]['gbs']:.1f} GB/s  "
+            f"{modes[mode]['us_per_layer']:.2f} us/layer")
+        if mode == "grouped":
+            head_launches, head_bytes, head_ms = launches, step_bytes, ms
+
+    kstats = kernel_stats(torch, eng, head_launches)
+    dominant = max(kstats, key=lambda k: kstats[k]["time_share"])
+    dk = kstats[dominant]
+    log(f"dominant kernel {dominant}: {dk['mean_us']:.2f} us/launch, {dk['gbs']:.1f} GB/s")
+    roofline = {"bound": "hbm", "achieved": dk["gbs"], "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": dk["gbs"] / PEAK_GBS, "traffic": None, "kernel": dominant,
+                "bytes_per_launch": dk["bytes_per_launch"], "mean_kernel_us": dk["mean_us"],
+                "launches_per_step": dk["launches_per_step"]}
+
+    extra = {}
+    if not args.no_extra:
+        for name, n, k, c, m in [("C1", 4096, 4096, QuantConfig(4, 128, False), 1),
+                                 ("C2", 11008, 4096, QuantConfig(8, None, True), 1),
+                                 ("C2_M4", 11008, 4096, QuantConfig(8, None, True), 4),
+                                 ("C3", 4096, 11008, QuantConfig(2, 64, False), 1)]:
+            key, res = single_config(torch, eng, name, n, k, c, m)
+            extra[key] = res
+            log(f"{key}: kernel {res['kernel_us']:.2f} us ({res['kernel_gbs']:.0f} GB/s), "
+                f"graph {res['us_per_call_graph']:.2f} us/call")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(torch, stack)
+        log(f"cpu baseline: {cpu['value']:.3f} GB/s on {cpu['cores']} threads ({time.perf_counter() - t0:.1f}s)")
+
+    gbs = head_bytes / (head_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head_ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int4 codes -> fp16 (q-z), fp16 x fp16 products, fp32 accumulate",
+        "data": "synthetic (seeded fp16 N(0,0.02) weights quantized on the GPU; fp16 N(0,1) activations)",
+        "config": {"workload": "C4: Llama-3-8B decoder linear set, INT4 g128 asym, M=1",
+                   "layers": args.layers, "batch": 1, "bytes_per_step": head_bytes,
+                   "launches_per_step": len(head_launches),
+                   "grouping": "per layer: q|k|v, o, gate|up, down (one launch each)"},
+        "pct_of_peak": 100 * gbs / PEAK_GBS,
+        "us_per_layer": head_ms * 1e3 / args.layers,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "modes": modes,
+        "kernels": kstats,
+        "single_configs": extra,
+    }
+    print(json.dumps(line, default=lambda o: sorted(o) if isinstance(o, set) else str(o)), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -13,7 +13,7 @@ Native code is built in-tree with `python -m dequant_project_amd.build`.
 
 from .packer import (PackedWeight, QuantConfig, dequantize, pack, quantize,  # noqa: F401
                      quantize_tensor, unpack)
-from .quant_linear import (MAX_M, PROJ, QuantLinear, dequantize_cuda, gemv,  # noqa: F401
+from .quant_linear import (MAX_M, PROJ, QuantLinear, dequantize_cuda, gemv, gemv_grouped,  # noqa: F401
                            quantize_model)
 
 __version__ = "0.1.0"

@@ -55,6 +55,22 @@ class DqTensor(ctypes.Structure):
     ]
 
 
+class DqGemvProblem(ctypes.Structure):
+    """struct dq_gemv_problem of include/dequant_hip.h."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("qweight", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("zeros", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("N", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("group_size", ctypes.c_int64),
+    ]
+
+
+DQ_MAX_BATCH = 16
 DQ_DTYPE_OTHER, DQ_DTYPE_INT32, DQ_DTYPE_FLOAT16, DQ_DTYPE_FLOAT32 = 0, 1, 2, 3
 DQ_OK, DQ_ERR_INVALID_ARGUMENT, DQ_ERR_UNSUPPORTED, DQ_ERR_LAUNCH, DQ_ERR_HIP = 0, 1, 2, 3, 4
 
@@ -69,6 +85,10 @@ SIGNATURES = {
     "dq_check_dequantize": (_I, [_T, _T, _T, _I64, _I64, _I, _I64]),
     "dq_check_unpack": (_I, [_T, _I64, _I64]),
     "dq_gemv": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I, _P]),
+    "dq_gemv_batched": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, _I, _I, _P]),
+    "dq_gemv_plan": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, ctypes.POINTER(ctypes.c_int),
+                          ctypes.POINTER(ctypes.c_int)]),
+    "dq_set_launch_events": (_I, [_P, _P]),
     "dq_dequantize": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P]),
     "dq_unpack": (_I, [_P, _P, _I64, _I64, _I64, _I, _P]),
     "dq_add_one": (_I, [_P, _P, _I64, _P]),

@@ -6,7 +6,7 @@
 //               (kernels/dequant_gemv.cu:230-283 check_weight, :310-317
 //               dequantize, :342-361 gemv). Pure host logic: no HIP call, so
 //               they run on machines without a GPU.
-//   dq_gemv / dq_dequantize / dq_unpack / dq_add_one
+//   dq_gemv / dq_gemv_batched / dq_dequantize / dq_unpack / dq_add_one
 //               validate the scalar contract of a raw-pointer call (the rules
 //               that do not need tensor metadata) and launch on `stream`.
 // Errors are reported as a status code plus a thread-local message.
@@ -18,6 +18,8 @@
 
 #include "dequant_hip.h"
 #include "dq_internal.h"
+
+static_assert(DQ_MAX_BATCH == dq::kMaxBatch, "batch limits of the ABI and the kernels differ");
 
 namespace {
 
@@ -159,6 +161,20 @@ int check_extent(int64_t N, int64_t K) {
   return DQ_OK;
 }
 
+// The scalar contract of one raw-pointer GEMV problem.
+int check_gemv_problem(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales, const uint16_t* zeros,
+                       const uint16_t* y, int64_t N, int64_t K, int64_t bits, int64_t group_size, int symmetric) {
+  if (!x || !qweight || !scales || !y)
+    return fail(DQ_ERR_INVALID_ARGUMENT, "x, qweight, scales and y must not be NULL");
+  if (!aligned16(x)) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+  int st = check_bits_group_k(bits, group_size, K);
+  if (st) return st;
+  if ((st = check_zeros_presence(zeros != nullptr, symmetric != 0))) return st;
+  if ((st = check_gemv_group(group_size, bits))) return st;
+  if (!aligned16(qweight)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
+  return check_extent(N, K);
+}
+
 int launch_status(hipError_t e) {
   if (e == hipSuccess) return DQ_OK;
   return fail(DQ_ERR_LAUNCH, cat("HIP launch failed: ", hipGetErrorString(e)));
@@ -237,18 +253,66 @@ int dq_gemv(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales, 
   g_error.clear();
   int st = check_m(M);
   if (st) return st;
-  if (!x || !qweight || !scales || !y)
-    return fail(DQ_ERR_INVALID_ARGUMENT, "x, qweight, scales and y must not be NULL");
-  if (!aligned16(x)) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
-  if ((st = check_bits_group_k(bits, group_size, K))) return st;
-  if ((st = check_zeros_presence(zeros != nullptr, symmetric != 0))) return st;
-  if ((st = check_gemv_group(group_size, bits))) return st;
-  if (!aligned16(qweight)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
-  if ((st = check_extent(N, K))) return st;
+  if ((st = check_gemv_problem(x, qweight, scales, zeros, y, N, K, bits, group_size, symmetric))) return st;
   if (N == 0) return DQ_OK;
-  dq::GemvProblem p{x, qweight, scales, zeros, y, M, N, K, static_cast<int>(bits), group_size,
-                    symmetric != 0, interleaved != 0};
-  return launch_status(dq::launch_gemv(p, reinterpret_cast<hipStream_t>(stream)));
+  const dq::GemvOperand op{x, qweight, scales, zeros, y, N, K, group_size};
+  return launch_status(dq::launch_gemv_batch(&op, 1, M, static_cast<int>(bits), symmetric != 0, interleaved != 0,
+                                             reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
+                    int interleaved, dq_stream_t stream) {
+  g_error.clear();
+  if (count < 1 || count > DQ_MAX_BATCH)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("count must be in [1, ", DQ_MAX_BATCH, "], got ", count));
+  if (!problems) return fail(DQ_ERR_INVALID_ARGUMENT, "problems must not be NULL");
+  int st = check_m(M);
+  if (st) return st;
+  dq::GemvOperand ops[DQ_MAX_BATCH];
+  int live = 0;
+  for (int i = 0; i < count; ++i) {
+    const dq_gemv_problem& p = problems[i];
+    if ((st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, bits, p.group_size,
+                                 symmetric))) {
+      g_error = cat("problem ", i, ": ", g_error);
+      return st;
+    }
+    if (p.N > 0) ops[live++] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
+  }
+  if (live == 0) return DQ_OK;
+  return launch_status(dq::launch_gemv_batch(ops, live, M, static_cast<int>(bits), symmetric != 0,
+                                             interleaved != 0, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* waves_per_tile,
+                 int* rows_per_tile) {
+  g_error.clear();
+  if (count < 1 || count > DQ_MAX_BATCH)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("count must be in [1, ", DQ_MAX_BATCH, "], got ", count));
+  if (!problems || !waves_per_tile || !rows_per_tile)
+    return fail(DQ_ERR_INVALID_ARGUMENT, "problems, waves_per_tile and rows_per_tile must not be NULL");
+  int st = check_m(M);
+  if (st) return st;
+  if (!(bits == 2 || bits == 4 || bits == 8))
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("bits must be 2, 4 or 8, got ", bits));
+  dq::GemvOperand ops[DQ_MAX_BATCH];
+  for (int i = 0; i < count; ++i) {
+    const dq_gemv_problem& p = problems[i];
+    if (p.K <= 0 || p.K % (128 / bits) != 0 || p.N < 0)
+      return fail(DQ_ERR_INVALID_ARGUMENT, cat("problem ", i, ": K=", p.K, " must be a positive multiple of ",
+                                               128 / bits, " and N=", p.N, " non-negative"));
+    ops[i] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
+  }
+  dq::plan_gemv_batch(ops, count, M, static_cast<int>(bits), waves_per_tile, rows_per_tile);
+  return DQ_OK;
+}
+
+int dq_set_launch_events(void* start_event, void* stop_event) {
+  g_error.clear();
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return fail(DQ_ERR_INVALID_ARGUMENT, "start_event and stop_event must both be set or both be NULL");
+  dq::set_launch_events(static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
+  return DQ_OK;
 }
 
 int dq_dequantize(const uint32_t* qweight, const uint16_t* scales, const uint16_t* zeros, uint16_t* out,

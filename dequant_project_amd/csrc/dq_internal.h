@@ -8,17 +8,33 @@
 
 namespace dq {
 
-struct GemvProblem {
+// Largest number of GEMV problems one launch takes (they travel by value in
+// the kernel argument block).
+constexpr int kMaxBatch = 16;
+
+// One y[M, N] = x[M, K] @ W^T problem of a (possibly grouped) launch.
+struct GemvOperand {
   const uint16_t* x;        // fp16 [M, K]
   const uint32_t* qweight;  // [N, K*bits/32]
   const uint16_t* scales;   // fp16 [N, K/group_size]
   const uint16_t* zeros;    // fp16 [N, K/group_size] or nullptr (symmetric)
   uint16_t* y;              // fp16 [M, N]
-  int64_t M, N, K;
-  int bits;
-  int64_t group_size;
-  bool symmetric, interleaved;
+  int64_t N, K, group_size;
 };
+
+// Profiling hook: when both events are non-null, the next GEMV launch on this
+// thread is issued with hipExtLaunchKernelGGL and these start/stop events
+// (they then bracket the kernel's own execution), after which they are cleared.
+void set_launch_events(hipEvent_t start, hipEvent_t stop);
+
+// Launch geometry a grouped GEMV would use: waves per tile along K for each
+// problem (wk[0..count-1]) and the launch's rows per tile (the kernel is
+// gemv_batched_kernel<bits, sym, inter, MT, rows, 2>).
+void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows);
+
+// All problems of one launch share M and the format (bits, symmetry, layout).
+hipError_t launch_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
+                             bool interleaved, hipStream_t stream);
 
 struct DequantProblem {
   const uint32_t* qweight;
@@ -31,7 +47,6 @@ struct DequantProblem {
   bool symmetric, interleaved;
 };
 
-hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream);
 hipError_t launch_dequantize(const DequantProblem& p, hipStream_t stream);
 hipError_t launch_unpack(const uint32_t* qweight, int32_t* out, int64_t N, int64_t K, int bits,
                          bool interleaved, hipStream_t stream);

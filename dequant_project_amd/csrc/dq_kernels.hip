@@ -14,11 +14,16 @@
 //   add_one_kernel     <- kernels/smoke.cu:9-13
 //
 // GEMV design (CDNA4, wave64):
-//   * One wave owns R consecutive output rows. Lane l walks the 16-byte chunks
-//     c = l, l+64, ... of those rows, so every global_load_dwordx4 of a wave
-//     reads 1 KiB of one row contiguously; the R rows' loads of a chunk column
-//     are issued back to back (R loads in flight per lane per step). A chunk
-//     holds 128/BITS codes of one group (group_size % (128/BITS) == 0).
+//   * One launch takes a list of up to 16 problems of one format (a single
+//     call is a list of one; q|k|v or gate|up of a decoder layer share one
+//     launch). Work is cut into tiles of R rows; a 256-thread block holds
+//     4/wk tiles and the wk waves of a tile split its K range, meeting in LDS.
+//   * Lane l walks the 16-byte chunks cb + l + 64t of its rows, so every
+//     global_load_dwordx4 of a wave reads 1 KiB of one row contiguously. A
+//     chunk holds 128/BITS codes of one group (group_size % (128/BITS) == 0).
+//     Every weight, scale and zero load of up to CMAX chunk columns is issued
+//     before any math (R*CMAX 16-byte loads in flight per lane); with M = 1
+//     the activations of those columns are gathered up front too.
 //   * Unpack to exact fp16 (code - zero) pairs in two VALU ops per pair:
 //       v_and_or_b32  (w & mask) | 0x64006400  -> fp16 (1024 + q * 2^p) in both
 //                     halves (q sits in mantissa bits [p, p+BITS), p <= 8);
@@ -32,20 +37,24 @@
 //     factorized scale), so the reference's elementwise fp32 error bound holds.
 //   * Zero points outside [-1024, 1024] (possible: the packer stores them
 //     unclamped) cannot use the exact fp16 form; such chunks take q exactly and
-//     subtract z * sum(x) in fp32 instead (wave-uniform branch, rare).
+//     subtract z * sum(x) in fp32 instead (uniform branch, rare).
 //   * Rows are finished with a DPP wave64 reduction (row_shr 1/2/4/8,
-//     row_bcast 15/31) instead of an LDS tree; lane 63 stores fp16 (RNE).
+//     row_bcast 15/31) instead of an LDS tree; fp16 (RNE) stores.
 //
 // All kernels are written for gfx950 only; no other target is built.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <algorithm>
 
 #include "dq_internal.h"
 
 namespace dq {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float f16_to_f32(uint16_t u) {
   return static_cast<float>(__builtin_bit_cast(_Float16, u));
@@ -177,36 +186,46 @@ __device__ __forceinline__ void load_x_pairs(const uint16_t* __restrict__ xw, h2
   }
 }
 
-template <int BITS, bool SYM, bool INTER, int MT, int R>
-__global__ void __launch_bounds__(kGemvThreads)
-gemv_kernel(const uint32_t* __restrict__ qweight, const uint16_t* __restrict__ scales,
-            const uint16_t* __restrict__ zeros, const uint16_t* __restrict__ x,
-            uint16_t* __restrict__ y, int M, int N, int K, int group_size) {
+// Launch-wide description of up to kMaxBatch problems (passed by value).
+struct KernelProblem {
+  const uint32_t* qweight;
+  const uint16_t* scales;
+  const uint16_t* zeros;
+  const uint16_t* x;
+  uint16_t* y;
+  int N, K;
+  int n_groups;          // K / group_size
+  int chunks_per_group;  // group_size / (128/BITS)
+  int n_chunks;          // K / (128/BITS)
+  int wk;                // waves sharing one tile along K (1, 2 or 4)
+  int tiles;             // ceil(N / R)
+};
+
+struct KernelBatch {
+  KernelProblem p[kMaxBatch];
+  int block_start[kMaxBatch + 1];  // blocks never mix problems
+  int count;
+  int M;
+};
+
+// One wave's share of a tile: rows row0 .. row0+R-1 of problem d, chunks
+// [cb, ce) of each row. Lane l takes chunks cb + l + 64 t. All weight, scale
+// and zero loads of a batch of CMAX columns are issued before any math, so a
+// lane has R*CMAX 16-byte loads in flight; for M = 1 the activations of the
+// batch are gathered up front as well.
+template <int BITS, bool SYM, bool INTER, int MT, int R, int CMAX>
+__device__ __forceinline__ void gemv_tile(const KernelProblem& d, int M, int row0, int cb, int ce, int lane,
+                                          float (&yacc)[R][MT]) {
   using F = Fmt<BITS>;
-  const int lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)) * R;
-  if (row0 >= N) return;  // whole wave leaves; no barrier in this kernel
-
-  const int n_chunks = K / F::CPL;
-  const int64_t words_per_row = K / F::PER;
-  const int ng = K / group_size;
-  const int chunks_per_group = group_size / F::CPL;
-
-  // Rows past N (last wave only) re-read row N-1 and are never stored.
+  const int64_t words_per_row = d.K / F::PER;
   const uint32_t* wrow[R];
-  int64_t meta_off[R];
+  int64_t moff[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, N - 1);
-    wrow[r] = qweight + row * words_per_row;
-    meta_off[r] = static_cast<int64_t>(row) * ng;
+    const int row = min(row0 + r, d.N - 1);  // rows past N re-read row N-1 and are never stored
+    wrow[r] = d.qweight + row * words_per_row;
+    moff[r] = static_cast<int64_t>(row) * d.n_groups;
   }
-
-  float yacc[R][MT];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int m = 0; m < MT; ++m) yacc[r][m] = 0.f;
 
   h2 pow_scale[F::NCLS];
 #pragma unroll
@@ -214,88 +233,164 @@ gemv_kernel(const uint32_t* __restrict__ qweight, const uint16_t* __restrict__ s
     pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
   const h2 ones = splat(static_cast<_Float16>(1.0f));
 
-  for (int c = lane; c < n_chunks; c += 64) {
-    uint4 wv[R];
+  for (int c0 = cb + lane; c0 < ce; c0 += 64 * CMAX) {
+    // ---- issue every load of the batch
+    u32x4 wv[CMAX][R];
+    uint16_t sraw[CMAX][R], zraw[CMAX][R];
+    h2 xq[MT == 1 ? CMAX : 1][MT == 1 ? 4 : 1][F::PAIRS];
 #pragma unroll
-    for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const uint4*>(wrow[r] + 4 * c);
-
-    const int g = c / chunks_per_group;
-    float sc[R], zf[R];
-    h2 off[R][F::NCLS];
-    bool any_inexact = false;
+    for (int t = 0; t < CMAX; ++t) {
+      const int c = c0 + 64 * t;
+      if (c < ce) {
+        const int g = c / d.chunks_per_group;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      sc[r] = f16_to_f32(scales[meta_off[r] + g]);
-      zf[r] = SYM ? static_cast<float>(F::BIAS) : f16_to_f32(zeros[meta_off[r] + g]);
-      const bool exact = class_offsets<BITS>(zf[r], off[r]);
-      if (!SYM) {
-        if (exact) zf[r] = 0.f;  // nothing left to subtract after the chunk
-        any_inexact |= !exact;
-      }
-    }
-    // wave-uniform: does any lane need sum(x) for an out-of-range zero point?
-    const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
-
-    float acc[R][MT];
-    float xsum[MT];
+        for (int r = 0; r < R; ++r) {
+          // weights are read exactly once: stream them past the caches
+          wv[t][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + 4 * c));
+          sraw[t][r] = d.scales[moff[r] + g];
+          if (!SYM) zraw[t][r] = d.zeros[moff[r] + g];
+        }
+        if constexpr (MT == 1) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      xsum[m] = 0.f;
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r][m] = 0.f;
-    }
-
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // the four words of the chunk
-      h2 xp[MT][F::PAIRS];
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (MT == 1 || m < M) {
-          load_x_pairs<BITS, INTER>(x + static_cast<int64_t>(m) * K + c * F::CPL + j * F::PER, xp[m]);
-          if (need_xsum) {
-#pragma unroll
-            for (int i = 0; i < F::PAIRS; ++i) xsum[m] = __builtin_amdgcn_fdot2(xp[m][i], ones, xsum[m], false);
-          }
+          for (int j = 0; j < 4; ++j) load_x_pairs<BITS, INTER>(d.x + c * F::CPL + j * F::PER, xq[t][j]);
         }
       }
+    }
+
+    // ---- math, one column at a time
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const uint32_t w = j == 0 ? wv[r].x : (j == 1 ? wv[r].y : (j == 2 ? wv[r].z : wv[r].w));
-        uint32_t mp[F::PAIRS];
-        magic_pairs<BITS>(w, mp);
-        h2 d[F::PAIRS];
+    for (int t = 0; t < CMAX; ++t) {
+      const int c = c0 + 64 * t;
+      if (c < ce) {
+        float sc[R], zf[R];
+        h2 off[R][F::NCLS];
+        bool any_inexact = false;
 #pragma unroll
-        for (int i = 0; i < F::PAIRS; ++i)
-          d[i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[r][F::cls(i)]);
+        for (int r = 0; r < R; ++r) {
+          sc[r] = f16_to_f32(sraw[t][r]);
+          zf[r] = SYM ? static_cast<float>(F::BIAS) : f16_to_f32(zraw[t][r]);
+          const bool exact = class_offsets<BITS>(zf[r], off[r]);
+          if (!SYM) {
+            if (exact) zf[r] = 0.f;
+            any_inexact |= !exact;
+          }
+        }
+        // uniform over the lanes of this column: does any need sum(x)?
+        const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
+
+        float acc[R][MT], xsum[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          if (MT == 1 || m < M) {
+          xsum[m] = 0.f;
 #pragma unroll
-            for (int i = 0; i < F::PAIRS; ++i) acc[r][m] = __builtin_amdgcn_fdot2(d[i], xp[m][i], acc[r][m], false);
+          for (int r = 0; r < R; ++r) acc[r][m] = 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h2 xp[MT][F::PAIRS];
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
+            if (MT == 1 || m < M) {
+              if constexpr (MT == 1) {
+#pragma unroll
+                for (int i = 0; i < F::PAIRS; ++i) xp[m][i] = xq[t][j][i];
+              } else {
+                load_x_pairs<BITS, INTER>(d.x + static_cast<int64_t>(m) * d.K + c * F::CPL + j * F::PER, xp[m]);
+              }
+              if (need_xsum) {
+#pragma unroll
+                for (int i = 0; i < F::PAIRS; ++i) xsum[m] = __builtin_amdgcn_fdot2(xp[m][i], ones, xsum[m], false);
+              }
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const uint32_t w = wv[t][r][j];
+            uint32_t mp[F::PAIRS];
+            magic_pairs<BITS>(w, mp);
+            h2 dq2[F::PAIRS];
+#pragma unroll
+            for (int i = 0; i < F::PAIRS; ++i)
+              dq2[i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[r][F::cls(i)]);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+              if (MT == 1 || m < M) {
+#pragma unroll
+                for (int i = 0; i < F::PAIRS; ++i) acc[r][m] = __builtin_amdgcn_fdot2(dq2[i], xp[m][i], acc[r][m], false);
+              }
+            }
           }
         }
-      }
-    }
-
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+        for (int r = 0; r < R; ++r) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        // symmetric: the bias is already inside (q - z); asymmetric with an
-        // in-range zero: zf == 0; out-of-range zero: subtract z * sum(x) here.
-        const float u = (!SYM && need_xsum) ? __builtin_fmaf(-zf[r], xsum[m], acc[r][m]) : acc[r][m];
-        yacc[r][m] = __builtin_fmaf(sc[r], u, yacc[r][m]);
+          for (int m = 0; m < MT; ++m) {
+            const float u = need_xsum ? __builtin_fmaf(-zf[r], xsum[m], acc[r][m]) : acc[r][m];
+            yacc[r][m] = __builtin_fmaf(sc[r], u, yacc[r][m]);
+          }
+        }
       }
     }
   }
+}
 
+// Grouped fused dequant + GEMV. A block (4 waves) belongs to one problem and
+// holds 4/wk tiles of it; a tile is R rows whose K range is split over wk
+// waves meeting in LDS. wk depends only on the problem's own K, so a problem
+// gives bit-identical results whether launched alone or in a group.
+template <int BITS, bool SYM, bool INTER, int MT, int R, int CMAX>
+__global__ void __launch_bounds__(kGemvThreads)
+gemv_batched_kernel(const KernelBatch b) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int p = 0;
+  while (p + 1 < b.count && static_cast<int>(blockIdx.x) >= b.block_start[p + 1]) ++p;
+  const KernelProblem& d = b.p[p];
+  const int wk = d.wk;
+  const int slot = wave / wk;
+  const int kw = wave - slot * wk;
+  const int tile = (static_cast<int>(blockIdx.x) - b.block_start[p]) * (kWavesPerBlock / wk) + slot;
+  const bool active = tile < d.tiles;
+  const int row0 = tile * R;
+
+  float yacc[R][MT];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float v = wave_sum_lane63(yacc[r][m]);
-      if (lane == 63 && row0 + r < N && (MT == 1 || m < M))
-        y[static_cast<int64_t>(m) * N + row0 + r] = f32_to_f16_rn(v);
+    for (int m = 0; m < MT; ++m) yacc[r][m] = 0.f;
+
+  if (active) {
+    const int per_wave = (d.n_chunks + wk - 1) / wk;
+    const int cb = kw * per_wave;
+    const int ce = min(d.n_chunks, cb + per_wave);
+    gemv_tile<BITS, SYM, INTER, MT, R, CMAX>(d, b.M, row0, cb, ce, lane, yacc);
+  }
+
+  if (wk == 1) {
+    // the wave owns the whole row: lane 63 stores
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float v = wave_sum_lane63(yacc[r][m]);
+        if (active && lane == 63 && row0 + r < d.N && (MT == 1 || m < b.M))
+          d.y[static_cast<int64_t>(m) * d.N + row0 + r] = f32_to_f16_rn(v);
+      }
+  } else {
+    __shared__ float partial[kWavesPerBlock][R * MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float v = wave_sum_lane63(yacc[r][m]);
+        if (lane == 63) partial[wave][r * MT + m] = v;
+      }
+    __syncthreads();  // every wave of the block reaches this (no early exit above)
+    if (active && kw == 0 && lane < R * MT) {
+      float v = 0.f;
+      for (int j = 0; j < wk; ++j) v += partial[wave + j][lane];
+      const int r = lane / MT, m = lane - (lane / MT) * MT;
+      if (row0 + r < d.N && m < b.M) d.y[static_cast<int64_t>(m) * d.N + row0 + r] = f32_to_f16_rn(v);
     }
   }
 }
@@ -370,6 +465,7 @@ add_one_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t n)
     out[i] = in[i] + 1.0f;
 }
 
+
 // ----------------------------------------------------------------- launchers
 namespace {
 
@@ -378,31 +474,92 @@ int64_t elementwise_blocks(int64_t items) {
   return b < 1 ? 1 : (b > 65536 ? 65536 : b);  // grid-stride loops cover the rest
 }
 
-template <int BITS, bool SYM, bool INTER>
-hipError_t launch_gemv_t(const GemvProblem& p, hipStream_t stream) {
-  if (p.M == 1) {
-    constexpr int R = 4;
-    const int rows_per_block = kWavesPerBlock * R;
-    const int blocks = static_cast<int>((p.N + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL((gemv_kernel<BITS, SYM, INTER, 1, R>), dim3(blocks), dim3(kGemvThreads), 0, stream,
-                       p.qweight, p.scales, p.zeros, p.x, p.y, static_cast<int>(p.M), static_cast<int>(p.N),
-                       static_cast<int>(p.K), static_cast<int>(p.group_size));
-  } else if (p.M <= 4) {
-    constexpr int R = 1;
-    const int rows_per_block = kWavesPerBlock * R;
-    const int blocks = static_cast<int>((p.N + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL((gemv_kernel<BITS, SYM, INTER, 4, R>), dim3(blocks), dim3(kGemvThreads), 0, stream,
-                       p.qweight, p.scales, p.zeros, p.x, p.y, static_cast<int>(p.M), static_cast<int>(p.N),
-                       static_cast<int>(p.K), static_cast<int>(p.group_size));
+// Launch geometry of a grouped GEMV:
+//   wk   per problem, waves per tile along K: the fewest of {1, 2, 4} that
+//        leave each lane at most CMAX 16-byte columns of its row (one batch of
+//        loads); it depends on the problem's K alone;
+//   R    rows per tile, shared by the launch: 4 (activations reused 4x) unless
+//        that leaves fewer than two waves per SIMD on the 1024 SIMDs of an
+//        MI355X, then 2 or 1. R does not change any row's arithmetic.
+constexpr int kCmax = 2;
+
+int waves_per_tile(int64_t K, int bits) {
+  const int64_t chunks = K / (128 / bits);
+  int wk = 1;
+  while (wk < 4 && (chunks + wk - 1) / wk > 64 * kCmax) wk *= 2;
+  return wk;
+}
+
+int rows_per_tile(const GemvOperand* ops, int count, int64_t M, int bits) {
+  if (M > 1) return 1;
+  constexpr int64_t kTargetWaves = 2048;
+  int R = 4;
+  for (; R > 1; R /= 2) {
+    int64_t waves = 0;
+    for (int i = 0; i < count; ++i) waves += (ops[i].N + R - 1) / R * waves_per_tile(ops[i].K, bits);
+    if (waves >= kTargetWaves) break;
+  }
+  return R;
+}
+
+thread_local hipEvent_t t_start_event = nullptr, t_stop_event = nullptr;
+
+template <int BITS, bool SYM, bool INTER, int MT, int R>
+hipError_t launch_batch_t(const KernelBatch& kb, hipStream_t stream) {
+  const int blocks = kb.block_start[kb.count];
+  if (t_start_event && t_stop_event) {
+    hipExtLaunchKernelGGL((gemv_batched_kernel<BITS, SYM, INTER, MT, R, kCmax>), dim3(blocks), dim3(kGemvThreads),
+                          0, stream, t_start_event, t_stop_event, 0, kb);
+    t_start_event = t_stop_event = nullptr;
   } else {
-    constexpr int R = 1;
-    const int rows_per_block = kWavesPerBlock * R;
-    const int blocks = static_cast<int>((p.N + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL((gemv_kernel<BITS, SYM, INTER, 8, R>), dim3(blocks), dim3(kGemvThreads), 0, stream,
-                       p.qweight, p.scales, p.zeros, p.x, p.y, static_cast<int>(p.M), static_cast<int>(p.N),
-                       static_cast<int>(p.K), static_cast<int>(p.group_size));
+    hipLaunchKernelGGL((gemv_batched_kernel<BITS, SYM, INTER, MT, R, kCmax>), dim3(blocks), dim3(kGemvThreads), 0,
+                       stream, kb);
   }
   return hipGetLastError();
+}
+
+template <int BITS, bool SYM, bool INTER, int MT, int R>
+hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+  constexpr int CPL = 128 / BITS;
+  KernelBatch kb{};
+  kb.count = count;
+  kb.M = static_cast<int>(M);
+  int blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    const GemvOperand& o = ops[i];
+    KernelProblem& k = kb.p[i];
+    k.qweight = o.qweight;
+    k.scales = o.scales;
+    k.zeros = o.zeros;
+    k.x = o.x;
+    k.y = o.y;
+    k.N = static_cast<int>(o.N);
+    k.K = static_cast<int>(o.K);
+    k.n_groups = static_cast<int>(o.K / o.group_size);
+    k.chunks_per_group = static_cast<int>(o.group_size / CPL);
+    k.n_chunks = static_cast<int>(o.K / CPL);
+    k.wk = waves_per_tile(o.K, BITS);
+    k.tiles = static_cast<int>((o.N + R - 1) / R);
+    const int tiles_per_block = kWavesPerBlock / k.wk;
+    kb.block_start[i] = blocks;
+    blocks += (k.tiles + tiles_per_block - 1) / tiles_per_block;
+  }
+  kb.block_start[count] = blocks;
+  if (blocks == 0) return hipSuccess;
+  return launch_batch_t<BITS, SYM, INTER, MT, R>(kb, stream);
+}
+
+template <int BITS, bool SYM, bool INTER>
+hipError_t launch_gemv_t(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+  if (M == 1) {
+    const int R = rows_per_tile(ops, count, M, BITS);
+    if (R == 4) return launch_gemv_r<BITS, SYM, INTER, 1, 4>(ops, count, M, stream);
+    if (R == 2) return launch_gemv_r<BITS, SYM, INTER, 1, 2>(ops, count, M, stream);
+    return launch_gemv_r<BITS, SYM, INTER, 1, 1>(ops, count, M, stream);
+  }
+  if (M == 2) return launch_gemv_r<BITS, SYM, INTER, 2, 1>(ops, count, M, stream);
+  if (M <= 4) return launch_gemv_r<BITS, SYM, INTER, 4, 1>(ops, count, M, stream);
+  return launch_gemv_r<BITS, SYM, INTER, 8, 1>(ops, count, M, stream);
 }
 
 template <int BITS, bool SYM, bool INTER>
@@ -443,9 +600,21 @@ hipError_t launch_unpack_t(const uint32_t* qweight, int32_t* out, int64_t N, int
     default: return hipErrorInvalidValue;                                      \
   }
 
-hipError_t launch_gemv(const GemvProblem& p, hipStream_t stream) {
-#define DQ_CALL_GEMV(B, S, I) launch_gemv_t<B, S, I>(p, stream)
-  DQ_DISPATCH_12(p.bits, p.symmetric, p.interleaved, DQ_CALL_GEMV)
+void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows) {
+  for (int i = 0; i < count; ++i) wk[i] = waves_per_tile(ops[i].K, bits);
+  *rows = rows_per_tile(ops, count, M, bits);
+}
+
+void set_launch_events(hipEvent_t start, hipEvent_t stop) {
+  t_start_event = start;
+  t_stop_event = stop;
+}
+
+hipError_t launch_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
+                             bool interleaved, hipStream_t stream) {
+  if (count < 1 || count > kMaxBatch) return hipErrorInvalidValue;
+#define DQ_CALL_GEMV(B, S, I) launch_gemv_t<B, S, I>(ops, count, M, stream)
+  DQ_DISPATCH_12(bits, symmetric, interleaved, DQ_CALL_GEMV)
 #undef DQ_CALL_GEMV
 }
 

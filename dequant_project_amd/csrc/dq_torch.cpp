@@ -12,6 +12,8 @@
 
 #include <optional>
 #include <stdexcept>
+#include <string>
+#include <vector>
 
 #include "dequant_hip.h"
 
@@ -75,6 +77,41 @@ torch::Tensor gemv(torch::Tensor x, torch::Tensor qweight, torch::Tensor scales,
   return y;
 }
 
+// Grouped launch of several GEMVs of one format and one M (no reference
+// counterpart; see dq_gemv_batched). Each problem is validated exactly as
+// gemv() validates its arguments.
+std::vector<torch::Tensor> gemv_batched(std::vector<torch::Tensor> xs, std::vector<torch::Tensor> qweights,
+                                        std::vector<torch::Tensor> scales,
+                                        std::vector<std::optional<torch::Tensor>> zeros, int64_t bits,
+                                        std::vector<int64_t> group_sizes, bool symmetric, bool interleaved) {
+  const size_t n = xs.size();
+  if (n == 0 || n > DQ_MAX_BATCH)
+    throw std::runtime_error("gemv_batched takes 1.." + std::to_string(DQ_MAX_BATCH) + " problems");
+  if (qweights.size() != n || scales.size() != n || zeros.size() != n || group_sizes.size() != n)
+    throw std::runtime_error("gemv_batched: xs, qweights, scales, zeros and group_sizes differ in length");
+  std::vector<dq_gemv_problem> probs(n);
+  std::vector<torch::Tensor> ys;
+  ys.reserve(n);
+  for (size_t i = 0; i < n; ++i) {
+    const dq_tensor dx = describe(xs[i]), dw = describe(qweights[i]), ds = describe(scales[i]);
+    dq_tensor dz{};
+    if (zeros[i]) dz = describe(*zeros[i]);
+    if (dq_check_gemv(&dx, &dw, &ds, zeros[i] ? &dz : nullptr, bits, group_sizes[i], symmetric) != DQ_OK)
+      throw std::runtime_error("problem " + std::to_string(i) + ": " + dq_last_error());
+    if (xs[i].size(0) != xs[0].size(0)) throw std::runtime_error("gemv_batched: all problems must share M");
+    if (xs[i].device() != xs[0].device()) throw std::runtime_error("gemv_batched: all problems must share a device");
+    ys.push_back(torch::empty({xs[i].size(0), qweights[i].size(0)}, xs[i].options()));
+    probs[i] = dq_gemv_problem{half_ptr(xs[i]), reinterpret_cast<const uint32_t*>(qweights[i].data_ptr()),
+                               half_ptr(scales[i]), zeros[i] ? half_ptr(*zeros[i]) : nullptr,
+                               reinterpret_cast<uint16_t*>(ys[i].data_ptr()), qweights[i].size(0),
+                               xs[i].size(1), group_sizes[i]};
+  }
+  const c10::DeviceGuard guard(xs[0].device());
+  raise_if(dq_gemv_batched(probs.data(), static_cast<int>(n), xs[0].size(0), bits, symmetric, interleaved,
+                           current_stream(xs[0])));
+  return ys;
+}
+
 // kernels/dequant_gemv.cu:310-337
 torch::Tensor dequantize(torch::Tensor qweight, torch::Tensor scales, std::optional<torch::Tensor> zeros,
                          int64_t bits, int64_t group_size, bool symmetric, bool interleaved, int64_t K) {
@@ -110,6 +147,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemv", &gemv, "packed-weight GEMV, fp16 [M,K] x [N,K]^T -> [M,N]", py::arg("x"), py::arg("qweight"),
         py::arg("scales"), py::arg("zeros"), py::arg("bits"), py::arg("group_size"), py::arg("symmetric"),
         py::arg("interleaved"));
+  m.def("gemv_batched", &gemv_batched, "grouped packed-weight GEMVs of one format in one launch",
+        py::arg("xs"), py::arg("qweights"), py::arg("scales"), py::arg("zeros"), py::arg("bits"),
+        py::arg("group_sizes"), py::arg("symmetric"), py::arg("interleaved"));
   m.def("dequantize", &dequantize, "materialize a packed weight as fp16 [N,K]", py::arg("qweight"),
         py::arg("scales"), py::arg("zeros"), py::arg("bits"), py::arg("group_size"), py::arg("symmetric"),
         py::arg("interleaved"), py::arg("K"));

@@ -45,6 +45,28 @@ def gemv(x, pw: PackedWeight):
     return y.view(*x.shape[:-1], n)
 
 
+def gemv_grouped(xs, pws):
+    """Several y_i = x_i @ W_i^T in ONE kernel launch (no reference counterpart).
+
+    All weights must share bits / symmetry / layout and all x_i the same
+    number of rows (at most MAX_M); up to 16 problems. Results are bit-identical
+    to calling gemv() per problem. This is the grouped decode launch: q|k|v
+    (same x) or gate|up of a Llama layer.
+    """
+    if not pws:
+        return []
+    cfg0 = pws[0].config
+    if any(pw.config.bits != cfg0.bits or pw.config.symmetric != cfg0.symmetric
+           or pw.config.layout != cfg0.layout for pw in pws):
+        raise ValueError("gemv_grouped: all weights must share bits, symmetric and layout")
+    x2s = [x.reshape(-1, pw.shape[1]).contiguous() for x, pw in zip(xs, pws)]
+    ys = _get_ext().gemv_batched(
+        x2s, [pw.qweight for pw in pws], [pw.scales for pw in pws], [pw.zeros for pw in pws],
+        cfg0.bits, [pw.config.effective_group_size(pw.shape[1]) for pw in pws], cfg0.symmetric,
+        cfg0.layout == "interleaved")
+    return [y.view(*x.shape[:-1], pw.shape[0]) for y, x, pw in zip(ys, xs, pws)]
+
+
 def dequantize_cuda(pw: PackedWeight):
     """fp16 [N, K] on the GPU, bit-exact with packer.dequantize."""
     n, k = pw.shape

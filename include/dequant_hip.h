@@ -130,6 +130,51 @@ int dq_gemv(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
             int64_t bits, int64_t group_size, int symmetric, int interleaved,
             dq_stream_t stream);
 
+/* One problem of a grouped GEMV launch: y[M, N] = x[M, K] @ W^T. */
+typedef struct dq_gemv_problem {
+  const uint16_t* x;        /* fp16 [M, K], 16-byte aligned */
+  const uint32_t* qweight;  /* [N, K*bits/32], 16-byte aligned */
+  const uint16_t* scales;   /* fp16 [N, K/group_size] */
+  const uint16_t* zeros;    /* fp16 [N, K/group_size], or NULL when symmetric */
+  uint16_t* y;              /* fp16 [M, N] */
+  int64_t N;
+  int64_t K;
+  int64_t group_size;       /* == K for per-channel */
+} dq_gemv_problem;
+
+/* Most problems one dq_gemv_batched call takes. */
+#define DQ_MAX_BATCH 16
+
+/* Grouped fused dequant + GEMV: up to DQ_MAX_BATCH independent problems that
+ * share M and the format (bits, symmetric, interleaved) in ONE kernel launch,
+ * e.g. q|k|v or gate|up of a decoder layer, whose inputs coincide, or the
+ * projections of several layers. Each problem obeys the rules of dq_gemv;
+ * results equal per-problem dq_gemv calls bit for bit. `problems` is a host
+ * array read during the call. No reference counterpart: the reference launches
+ * one kernel per linear (dequant/quant_linear.py:72-82); this is the grouped
+ * launch its decode path would use to avoid per-launch overhead. */
+int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
+                    int interleaved, dq_stream_t stream);
+
+/* Geometry the launch of these problems would use (no reference
+ * counterpart): for each problem i, waves_per_tile[i] waves (1, 2 or 4) share
+ * one tile along K -- a function of that problem's K only -- and the launch
+ * uses *rows_per_tile output rows per tile. The kernel instance is named
+ * gemv_batched_kernel<bits, symmetric, interleaved, MT, rows_per_tile, 2> with
+ * MT = 1, 2, 4 or 8 (the smallest >= M). Pure host logic, for profiling and
+ * tuning tools. waves_per_tile must hold `count` ints. */
+int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* waves_per_tile,
+                 int* rows_per_tile);
+
+/* Profiling hook (no reference counterpart; the reference profiles with
+ * Nsight, scripts/bench_dequant_kernel.py:205-229): when both are non-NULL
+ * hipEvent_t handles, the NEXT dq_gemv / dq_gemv_batched launch on the calling
+ * thread records `start_event` when its kernel starts executing and
+ * `stop_event` when it ends (hipExtLaunchKernelGGL), so the pair times the
+ * kernel alone, without launch gaps. The setting is consumed by that launch;
+ * passing NULL, NULL clears it. Do not use while capturing a HIP graph. */
+int dq_set_launch_events(void* start_event, void* stop_event);
+
 /* out[N, K] = fp16_rn( (code - offset) * scale ), bit-exact with the
  * reference's packer.dequantize (dequant/packer.py:177-189). Replaces
  * dequant_cuda.dequantize (kernels/dequant_gemv.cu:310-337, kernel :113-140).

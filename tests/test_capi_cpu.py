@@ -193,3 +193,46 @@ def test_torch_binding_rejects_cpu_tensors_with_reference_messages():
                        interleaved=False, K=256)
     with pytest.raises(RuntimeError, match="CUDA tensor"):
         ext.unpack(qweight=qw, bits=4, interleaved=False, K=256)
+
+
+def test_gemv_plan_geometry():
+    """dq_gemv_plan (host logic): waves per tile from K alone, rows per tile from the total work."""
+    lib = _native.capi()
+
+    def plan(shapes, m=1, bits=4):
+        arr = (_native.DqGemvProblem * len(shapes))()
+        for i, (n, k) in enumerate(shapes):
+            arr[i].N, arr[i].K, arr[i].group_size = n, k, 128
+        wk, rows = (ctypes.c_int * len(shapes))(), ctypes.c_int()
+        assert lib.dq_gemv_plan(arr, len(shapes), m, bits, wk, ctypes.byref(rows)) == 0, lib.dq_last_error()
+        return list(wk), rows.value
+
+    # INT4: 32 codes per 16-byte chunk; a wave covers 64 lanes x 2 chunks = 4096 codes
+    assert plan([(14336, 4096)]) == ([1], 4)
+    assert plan([(4096, 14336)]) == ([4], 4)        # 448 chunks -> 4 waves per tile
+    assert plan([(4096, 4096)]) == ([1], 2)         # 4096/4 tiles would leave < 2048 waves
+    assert plan([(1024, 4096)]) == ([1], 1)
+    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([1, 1, 1], 2)
+    assert plan([(4096, 11008)], bits=2) == ([2], 4)  # 172 chunks of 64 codes: 2 waves x 1024 tiles
+    assert plan([(4096, 4096)], m=4) == ([1], 1)
+    arr = (_native.DqGemvProblem * 1)()
+    arr[0].N, arr[0].K = 8, 100
+    wk, rows = (ctypes.c_int * 1)(), ctypes.c_int()
+    assert lib.dq_gemv_plan(arr, 1, 1, 4, wk, ctypes.byref(rows)) == 1
+    assert b"must be a positive multiple of 32" in lib.dq_last_error()
+
+
+def test_gemv_batched_validation():
+    lib = _native.capi()
+    arr = (_native.DqGemvProblem * 2)()
+    assert lib.dq_gemv_batched(arr, 0, 1, 4, 1, 0, None) == 1
+    assert lib.dq_last_error() == b"count must be in [1, 16], got 0"
+    assert lib.dq_gemv_batched(arr, 2, 9, 4, 1, 0, None) == 2
+    for i in range(2):
+        arr[i].x = arr[i].qweight = arr[i].scales = arr[i].y = 0x1000
+        arr[i].N, arr[i].K, arr[i].group_size = 4, 256, 128
+    arr[1].K = 250
+    assert lib.dq_gemv_batched(arr, 2, 1, 4, 1, 0, None) == 1
+    assert lib.dq_last_error() == b"problem 1: K=250 is not divisible by group_size=128"
+    assert lib.dq_set_launch_events(ctypes.c_void_p(0x10), None) == 1
+    assert lib.dq_set_launch_events(None, None) == 0
