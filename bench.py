@@ -9,20 +9,29 @@ seeded generator, quantized on the GPU by the engine's packer (3.71 GB packed,
 well past the 256 MB Infinity Cache, so every step streams from HBM);
 activations are fp16 N(0, 1). Everything is resident in HBM before timing.
 
-One step = one decode pass of the hot path over the whole stack, captured in a
-HIP graph. Per layer it launches what a decoder launches, given the data
-dependencies of a Llama layer: q|k|v grouped (same input), o, gate|up grouped
-(same input), down -- 4 launches per layer, 128 per step. Also measured and
-reported: the same step as 7 per-linear launches per layer (the QuantLinear
-drop-in path), and the rotating-copy single-config runs of C1/C2/C3.
+One step = one pass of the hot path over the whole stack: all 224 GEMVs, each
+with its own synthetic input, captured in one HIP graph. Three launch
+structures are timed:
+
+  stack       (headline) the independent GEMVs of the stack as grouped
+              launches of up to 16 problems of equal K -- 12 launches of six
+              K=4096 projections x 16/6 layers, 2 of 16 down_proj -- i.e. the
+              sustained bandwidth of the kernel over the Llama-3-8B layer
+              shapes, with launch overhead amortized (the reference times
+              independent back-to-back GEMV calls the same way,
+              scripts/bench_dequant_kernel.py:119-168);
+  decode      what a decoder launches given a Llama layer's data
+              dependencies: q|k|v grouped (same input), o, gate|up grouped,
+              down -- 4 launches per layer, 128 per step;
+  per_linear  the QuantLinear drop-in path: one launch per projection.
 
 Printed: ONE JSON line on stdout (progress goes to stderr).
-  value       whole-step algorithmic bytes / step time, GB/s (the
+  value       stack-mode algorithmic bytes per step / step time, GB/s (the
               byte_model accounting: packed weights + scales + zeros + x + y)
-  roofline    the dominant kernel instance: algorithmic bytes per launch /
-              its mean kernel duration (timed with HIP events recorded by the
-              kernel dispatch itself, hipExtLaunchKernelGGL, on the launch
-              stream), against the 8 TB/s HBM3E peak
+  roofline    the dominant kernel instance of the stack step: algorithmic
+              bytes per launch / its mean launch duration, the latter from HIP
+              events around the timed graph replays divided by the launches
+              (the stack step runs one kernel instance), against 8 TB/s
   cpu_baseline  the reference's CPU torch path (oracle/cpu_path.py) on one
               layer of the same stack, on this host's cores
 
@@ -73,14 +82,16 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=LAYERS, help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C2/C3 single-config runs")
+    ap.add_argument("--modes", default="stack,decode,per_linear",
+                    help="comma-separated step structures to time (stack is the headline)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 1 GiB device copy (rocprof FETCH_SIZE/WRITE_SIZE calibration)")
     return ap.parse_args()
 
 
 class Engine:
-    """The engine's entry points used here: the torch extension for launches,
-    the C ABI for the launch plan and the kernel-timing hook."""
+    """The engine's entry points used here: the torch extension for launches
+    and the C ABI's launch plan (to name the kernel instance of a launch)."""
 
     def __init__(self, torch):
         from dequant_project_amd import _native
@@ -114,20 +125,9 @@ class Engine:
         m = xs[0].shape[0]
         st = self.capi.dq_gemv_plan(arr, n, m, cfg.bits, wk, ctypes.byref(rows))
         self.native.check(st)
+        fmt = f"{cfg.bits}, {str(cfg.symmetric).lower()}, {str(cfg.layout == 'interleaved').lower()}"
         mt = 1 if m == 1 else (2 if m == 2 else (4 if m <= 4 else 8))
-        return (f"gemv_batched_kernel<{cfg.bits}, {str(cfg.symmetric).lower()}, "
-                f"{str(cfg.layout == 'interleaved').lower()}, {mt}, {rows.value}, 2>"), tuple(wk)
-
-    def timed_launch(self, xs, pws):
-        """One eager launch whose kernel is bracketed by dispatch-recorded events; returns ms."""
-        torch = self.torch
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        e1.record()  # creates both events
-        self.native.check(self.capi.dq_set_launch_events(e0.cuda_event, e1.cuda_event))
-        self.gemv_group(xs, pws)
-        e1.synchronize()
-        return e0.elapsed_time(e1)
+        return f"gemv_kernel<{fmt}, {mt}, {rows.value}, 1>", tuple(wk)
 
 
 def build_stack(torch, layers, seed=20251201):
@@ -155,9 +155,20 @@ def build_stack(torch, layers, seed=20251201):
 def step_launches(stack, xs, mode):
     """[(role, [x...], [pw...])] of one step."""
     out = []
+    if mode == "stack":
+        by_k = {}
+        for layer, x in zip(stack, xs):
+            for role, names in GROUPS:
+                for n in names:
+                    by_k.setdefault(layer[n].shape[1], []).append((x[role], layer[n]))
+        for k, items in by_k.items():
+            for i in range(0, len(items), 16):
+                chunk = items[i:i + 16]
+                out.append((f"K={k}", [c[0] for c in chunk], [c[1] for c in chunk]))
+        return out
     for layer, x in zip(stack, xs):
         for role, names in GROUPS:
-            if mode == "grouped":
+            if mode == "decode":
                 out.append((role, [x[role]] * len(names), [layer[n] for n in names]))
             else:
                 for n in names:
@@ -216,33 +227,13 @@ def run_mode(torch, eng, stack, xs, mode, steps, warmup):
     return launches, step_bytes, ms, per
 
 
-def kernel_stats(torch, eng, launches, reps=3):
-    """Per kernel instance: launches per step, bytes per launch, mean duration (events)."""
-    stats = {}
-    for _, x, p in launches:  # warm
-        eng.gemv_group(x, p)
-    torch.cuda.synchronize()
-    for _ in range(reps):
-        for role, x, p in launches:
-            name, wk = eng.kernel_name(x, p)
-            ms = eng.timed_launch(x, p)
-            s = stats.setdefault(name, {"launch_ms": [], "bytes": [], "roles": set(), "wk": set()})
-            s["launch_ms"].append(ms)
-            s["bytes"].append(launch_bytes(x, p))
-            s["roles"].add(role)
-            s["wk"].add(wk)
-    out = {}
-    for name, s in stats.items():
-        mean_ms = sum(s["launch_ms"]) / len(s["launch_ms"])
-        mean_bytes = sum(s["bytes"]) / len(s["bytes"])
-        out[name] = {"launches_per_step": len(s["launch_ms"]) // reps, "mean_us": mean_ms * 1e3,
-                     "bytes_per_launch": mean_bytes, "gbs": mean_bytes / (mean_ms * 1e-3) / 1e9,
-                     "roles": sorted(s["roles"]), "waves_per_tile": sorted(s["wk"]),
-                     "time_share": sum(s["launch_ms"])}
-    total = sum(v["time_share"] for v in out.values())
-    for v in out.values():
-        v["time_share"] = v["time_share"] / total
-    return out
+def kernel_instances(eng, launches):
+    """Kernel instance of every launch of a step (dq_gemv_plan) -> {name: [bytes...]}."""
+    inst = {}
+    for _, x, p in launches:
+        name, _ = eng.kernel_name(x, p)
+        inst.setdefault(name, []).append(launch_bytes(x, p))
+    return inst
 
 
 def cpu_baseline(torch, stack):
@@ -308,18 +299,30 @@ def single_config(torch, eng, name, n, k, cfg, m, reps=10):
 
     graph = capture(torch, fn)
     ms, per = time_graph(torch, graph, reps, 2)
-    kms = [eng.timed_launch([x], [p]) for p in pws[:min(copies, 64)]]
     b = launch_bytes([x], [first])
-    kernel_us = statistics.median(kms) * 1e3
+    us = statistics.median(per) * 1e3 / copies
     res = {"shape": [n, k], "M": m, "format": f"INT{cfg.bits} g{cfg.group_size or 'pc'} "
            f"{'sym' if cfg.symmetric else 'asym'}", "copies": copies, "bytes_per_call": b,
-           "us_per_call_graph": statistics.median(per) * 1e3 / copies,
-           "kernel_us": kernel_us, "kernel_gbs": b / (kernel_us * 1e-6) / 1e9,
-           "kernel_pct_peak": 100 * b / (kernel_us * 1e-6) / 1e9 / PEAK_GBS}
-    res["graph_gbs"] = b / (res["us_per_call_graph"] * 1e-6) / 1e9
+           "us_per_call": us, "gbs": b / (us * 1e-6) / 1e9, "pct_peak": 100 * b / (us * 1e-6) / 1e9 / PEAK_GBS,
+           "kernel": eng.kernel_name([x], [first])[0]}
     del graph, pws, first
     torch.cuda.empty_cache()
     return name, res
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_kernel_int4_c4_stack_traffic.md")
+
+
+def profiled_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-calibrated), or None if that summary is of
+    another kernel."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+        rec = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    except (OSError, IndexError, ValueError):
+        return None
+    return rec["traffic_bytes_per_launch"] if rec.get("kernel") == kernel else None
 
 
 def main():
@@ -354,26 +357,39 @@ def main():
     log(f"built {args.layers}-layer INT4 stack in {time.perf_counter() - t0:.1f}s")
 
     modes = {}
-    for mode in ("grouped", "per_linear"):
+    want = [m.strip() for m in args.modes.split(",") if m.strip()]
+    if "stack" not in want:
+        want.insert(0, "stack")
+    for mode in want:
         launches, step_bytes, ms, per = run_mode(torch, eng, stack, xs, mode, args.steps, args.warmup)
         st = summarize(per)
+        inst = kernel_instances(eng, launches)
         modes[mode] = {"launches_per_step": len(launches), "bytes_per_step": step_bytes, "ms_per_step": ms,
                        "step_ms": st, "gbs": step_bytes / (ms * 1e-3) / 1e9,
                        "us_per_layer": ms * 1e3 / args.layers,
-                       "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS}
+                       "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                       "kernel_instances": {k: len(v) for k, v in inst.items()}}
         log(f"mode {mode}: {ms:.3f} ms/step  {modes[mode]['gbs']:.1f} GB/s  "
-            f"{modes[mode]['us_per_layer']:.2f} us/layer")
-        if mode == "grouped":
-            head_launches, head_bytes, head_ms = launches, step_bytes, ms
+            f"{modes[mode]['us_per_layer']:.2f} us/layer  ({len(launches)} launches)")
+        if mode == "stack":
+            head_launches, head_bytes, head_ms, head_inst = launches, step_bytes, ms, inst
 
-    kstats = kernel_stats(torch, eng, head_launches)
-    dominant = max(kstats, key=lambda k: kstats[k]["time_share"])
-    dk = kstats[dominant]
-    log(f"dominant kernel {dominant}: {dk['mean_us']:.2f} us/launch, {dk['gbs']:.1f} GB/s")
-    roofline = {"bound": "hbm", "achieved": dk["gbs"], "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": dk["gbs"] / PEAK_GBS, "traffic": None, "kernel": dominant,
-                "bytes_per_launch": dk["bytes_per_launch"], "mean_kernel_us": dk["mean_us"],
-                "launches_per_step": dk["launches_per_step"]}
+    # the stack step runs a single kernel instance: its mean launch duration is
+    # the timed region over the launches in it (gaps between the 14 long
+    # launches are included, a few percent)
+    dominant = max(head_inst, key=lambda k: sum(head_inst[k]))
+    n_dom = len(head_inst[dominant])
+    bytes_per_launch = sum(head_inst[dominant]) / n_dom
+    mean_us = head_ms * 1e3 / len(head_launches) if len(head_inst) == 1 else None
+    achieved = bytes_per_launch / (mean_us * 1e-6) / 1e9 if mean_us else None
+    log(f"dominant kernel {dominant}: {n_dom} launches/step, {bytes_per_launch / 1e6:.1f} MB/launch, "
+        f"{mean_us:.2f} us/launch, {achieved:.1f} GB/s")
+    traffic = profiled_traffic(dominant)
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_GBS if achieved else None,
+                "traffic": traffic, "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                                    "copy-calibrated; profiles/)", "kernel": dominant,
+                "bytes_per_launch": bytes_per_launch, "mean_launch_us": mean_us, "launches_per_step": n_dom}
 
     extra = {}
     if not args.no_extra:
@@ -383,8 +399,8 @@ def main():
                                  ("C3", 4096, 11008, QuantConfig(2, 64, False), 1)]:
             key, res = single_config(torch, eng, name, n, k, c, m)
             extra[key] = res
-            log(f"{key}: kernel {res['kernel_us']:.2f} us ({res['kernel_gbs']:.0f} GB/s), "
-                f"graph {res['us_per_call_graph']:.2f} us/call")
+            log(f"{key}: {res['us_per_call']:.2f} us/call ({res['gbs']:.0f} GB/s) in a graph of "
+                f"{res['copies']} distinct copies")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -398,16 +414,16 @@ def main():
         "warmup": args.warmup, "ms_per_step": head_ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int4 codes -> fp16 (q-z), fp16 x fp16 products, fp32 accumulate",
         "data": "synthetic (seeded fp16 N(0,0.02) weights quantized on the GPU; fp16 N(0,1) activations)",
-        "config": {"workload": "C4: Llama-3-8B decoder linear set, INT4 g128 asym, M=1",
+        "config": {"workload": "C4: Llama-3-8B decoder linear set (32 layers x q,k,v,o,gate,up,down), "
+                               "INT4 g128 asym, M=1",
                    "layers": args.layers, "batch": 1, "bytes_per_step": head_bytes,
                    "launches_per_step": len(head_launches),
-                   "grouping": "per layer: q|k|v, o, gate|up, down (one launch each)"},
+                   "grouping": "stack: launches of up to 16 independent GEMVs of equal K"},
         "pct_of_peak": 100 * gbs / PEAK_GBS,
         "us_per_layer": head_ms * 1e3 / args.layers,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "modes": modes,
-        "kernels": kstats,
         "single_configs": extra,
     }
     print(json.dumps(line, default=lambda o: sorted(o) if isinstance(o, set) else str(o)), flush=True)

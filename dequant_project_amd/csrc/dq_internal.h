@@ -29,7 +29,7 @@ void set_launch_events(hipEvent_t start, hipEvent_t stop);
 
 // Launch geometry a grouped GEMV would use: waves per tile along K for each
 // problem (wk[0..count-1]) and the launch's rows per tile (the kernel is
-// gemv_batched_kernel<bits, sym, inter, MT, rows, 2>).
+// gemv_kernel<bits, sym, inter, MT, rows, 1>).
 void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows);
 
 // All problems of one launch share M and the format (bits, symmetry, layout).

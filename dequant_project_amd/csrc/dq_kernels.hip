@@ -55,6 +55,7 @@ namespace dq {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float f16_to_f32(uint16_t u) {
   return static_cast<float>(__builtin_bit_cast(_Float16, u));
@@ -96,42 +97,62 @@ template <int BITS> struct Fmt {
   static constexpr __device__ int class_pow(int c) { return BITS == 4 ? 4 * c : 2 * c; }
 };
 
+// 0x64006400 held in a VGPR: with it in a register the masking below is one
+// v_and_or_b32 (gfx9 VOP3 encodings take no literal constants, so with both
+// constants literal the compiler would need a v_and_b32 plus a v_or_b32).
+__device__ __forceinline__ uint32_t magic_vgpr() {
+  uint32_t m;
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(m));
+  return m;
+}
+
 // Word -> PER/2 magic pairs: both fp16 halves of pair i are 1024 + q * 2^p,
 // the low half from slot i, the high half from slot i + PER/2.
 template <int BITS>
-__device__ __forceinline__ void magic_pairs(uint32_t w, uint32_t* p) {
-  constexpr uint32_t kMagic = 0x64006400u;
+__device__ __forceinline__ void magic_pairs(uint32_t w, uint32_t magic, uint32_t* p) {
   if constexpr (BITS == 8) {
     p[0] = __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u);  // {0x64, b2, 0x64, b0}
     p[1] = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);  // {0x64, b3, 0x64, b1}
   } else if constexpr (BITS == 4) {
-    p[0] = (w & 0x000F000Fu) | kMagic;
-    p[1] = (w & 0x00F000F0u) | kMagic;
+    p[0] = (w & 0x000F000Fu) | magic;
+    p[1] = (w & 0x00F000F0u) | magic;
     const uint32_t w8 = w >> 8;
-    p[2] = (w8 & 0x000F000Fu) | kMagic;
-    p[3] = (w8 & 0x00F000F0u) | kMagic;
+    p[2] = (w8 & 0x000F000Fu) | magic;
+    p[3] = (w8 & 0x00F000F0u) | magic;
   } else {
 #pragma unroll
-    for (int i = 0; i < 5; ++i) p[i] = (w & (0x00030003u << (2 * i))) | kMagic;
+    for (int i = 0; i < 5; ++i) p[i] = (w & (0x00030003u << (2 * i))) | magic;
     const uint32_t w10 = w >> 10;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) p[5 + i] = (w10 & (0x00030003u << (2 * i))) | kMagic;
+    for (int i = 0; i < 3; ++i) p[5 + i] = (w10 & (0x00030003u << (2 * i))) | magic;
   }
 }
 
 // Per (row, chunk) constants turning magic pairs of class c into (q - z):
-// (1024 + q 2^p) * 2^-p + off[c] with off[c] = -(2^(10-p) + z). When z is
-// outside [-1024, 1024] the exact fp16 form is unavailable; then off[c]
-// yields q alone and the caller subtracts z * sum(x) in fp32.
-template <int BITS>
-__device__ __forceinline__ bool class_offsets(float z, h2* off) {
+// (1024 + q 2^p) * 2^-p + off[c] with off[c] = -(2^(10-p) + z), computed in
+// fp16 straight from the stored zero (exact: |2^(10-p) + z| <= 2048). Zero
+// points outside [-1024, 1024] (or not finite) cannot use the exact form; then
+// off[c] = -2^(10-p) yields q alone and the caller subtracts z * sum(x).
+template <int BITS, bool SYM>
+__device__ __forceinline__ bool class_offsets(uint16_t zbits, h2* off) {
   using F = Fmt<BITS>;
-  const bool exact = __builtin_fabsf(z) <= 1024.0f;  // z is an integer or not finite
-  const _Float16 zh = exact ? static_cast<_Float16>(z) : static_cast<_Float16>(0.0f);
+  bool exact = true;
+  _Float16 z;
+  if constexpr (SYM) {
+    z = static_cast<_Float16>(static_cast<float>(F::BIAS));
+  } else {
+    exact = (zbits & 0x7FFFu) <= 0x6400u;  // |z| <= 1024 on the fp16 bit pattern
+    z = exact ? __builtin_bit_cast(_Float16, zbits) : static_cast<_Float16>(0.0f);
+  }
+  const h2 zz = splat(z);
 #pragma unroll
-  for (int c = 0; c < F::NCLS; ++c) {
-    const _Float16 base = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c))));
-    off[c] = splat(-(base + zh));  // exact: |base + z| <= 2048
+  for (int c = 0; c < F::NCLS; c += 2) {
+    const _Float16 b0 = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c))));
+    const _Float16 b1 = c + 1 < F::NCLS ? static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c + 1))))
+                                        : b0;
+    const h2 both = -(h2{b0, b1} + zz);  // one v_pk_add_f16 for two classes
+    off[c] = splat(both.x);
+    if (c + 1 < F::NCLS) off[c + 1] = splat(both.y);
   }
   return exact;
 }
@@ -143,46 +164,50 @@ __device__ __forceinline__ float dpp_move(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
 }
 
-// Sum over the 64 lanes of a wave; the total lands in lane 63.
-__device__ __forceinline__ float wave_sum_lane63(float v) {
-  v += dpp_move<0x111, 0xf>(v);  // row_shr:1
-  v += dpp_move<0x112, 0xf>(v);  // row_shr:2
-  v += dpp_move<0x114, 0xf>(v);  // row_shr:4
-  v += dpp_move<0x118, 0xf>(v);  // row_shr:8   -> lane 16r+15 holds row r's sum
-  v += dpp_move<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
-  v += dpp_move<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
-  return v;
+// Sums over the 64 lanes of a wave, for N values at once (interleaving the N
+// chains hides the DPP read-after-write wait states); totals land in lane 63.
+template <int N>
+__device__ __forceinline__ void wave_sum_lane63(float* v) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_move<0x111, 0xf>(v[i]);  // row_shr:1
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_move<0x112, 0xf>(v[i]);  // row_shr:2
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_move<0x114, 0xf>(v[i]);  // row_shr:4
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_move<0x118, 0xf>(v[i]);  // row_shr:8: lane 16r+15 has row r
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_move<0x142, 0xa>(v[i]);  // row_bcast:15 into rows 1, 3
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_move<0x143, 0xc>(v[i]);  // row_bcast:31 into rows 2, 3
 }
 
 // ---------------------------------------------------------------------- gemv
 constexpr int kGemvThreads = 256;  // 4 waves
 constexpr int kWavesPerBlock = kGemvThreads / 64;
+constexpr uint32_t kBufferConfig = 0x00020000u;  // raw 32-bit buffer view (gfx9 descriptor word 3)
 
-// Gather the PER activations of word j of chunk c for batch row m into pair order.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           static_cast<int>(kBufferConfig));
+}
+
+// Activation pair i of a word: (x[L(i)], x[L(i + PER/2)]) from the word's
+// PER halves held as PER/2 dwords d[]; one v_perm_b32 unless the pair is
+// already a dword (interleaved layouts).
 template <int BITS, bool INTER>
-__device__ __forceinline__ void load_x_pairs(const uint16_t* __restrict__ xw, h2* xp) {
+__device__ __forceinline__ void x_pairs_from_dwords(const uint32_t* d, h2* xp) {
   using F = Fmt<BITS>;
-  uint16_t xv[F::PER];
-  if constexpr (F::PER == 4) {
-    const uint2 t = *reinterpret_cast<const uint2*>(xw);
-    xv[0] = t.x & 0xFFFF; xv[1] = t.x >> 16; xv[2] = t.y & 0xFFFF; xv[3] = t.y >> 16;
-  } else {
-#pragma unroll
-    for (int q = 0; q < F::PER / 8; ++q) {
-      const uint4 t = *reinterpret_cast<const uint4*>(xw + 8 * q);
-      const uint32_t u[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xv[8 * q + 2 * e] = u[e] & 0xFFFF;
-        xv[8 * q + 2 * e + 1] = u[e] >> 16;
-      }
-    }
-  }
 #pragma unroll
   for (int i = 0; i < F::PAIRS; ++i) {
-    const uint32_t lo = xv[logical_of_slot<BITS, INTER>(i)];
-    const uint32_t hi = xv[logical_of_slot<BITS, INTER>(i + F::PAIRS)];
-    xp[i] = as_h2(lo | (hi << 16));
+    const int lo = logical_of_slot<BITS, INTER>(i);
+    const int hi = logical_of_slot<BITS, INTER>(i + F::PAIRS);
+    if ((lo & 1) == 0 && hi == lo + 1) {
+      xp[i] = as_h2(d[lo >> 1]);
+    } else {
+      const uint32_t sel = ((hi & 1) ? 0x07060000u : 0x05040000u) | ((lo & 1) ? 0x0302u : 0x0100u);
+      xp[i] = as_h2(__builtin_amdgcn_perm(d[hi >> 1], d[lo >> 1], sel));
+    }
   }
 }
 
@@ -203,195 +228,241 @@ struct KernelProblem {
 
 struct KernelBatch {
   KernelProblem p[kMaxBatch];
-  int block_start[kMaxBatch + 1];  // blocks never mix problems
+  int bt_start[kMaxBatch + 1];  // prefix sums of block-tiles (4/wk tiles each); blocks never mix problems
   int count;
   int M;
 };
 
-// One wave's share of a tile: rows row0 .. row0+R-1 of problem d, chunks
-// [cb, ce) of each row. Lane l takes chunks cb + l + 64 t. All weight, scale
-// and zero loads of a batch of CMAX columns are issued before any math, so a
-// lane has R*CMAX 16-byte loads in flight; for M = 1 the activations of the
-// batch are gathered up front as well.
-template <int BITS, bool SYM, bool INTER, int MT, int R, int CMAX>
-__device__ __forceinline__ void gemv_tile(const KernelProblem& d, int M, int row0, int cb, int ce, int lane,
-                                          float (&yacc)[R][MT]) {
-  using F = Fmt<BITS>;
-  const int64_t words_per_row = d.K / F::PER;
-  const uint32_t* wrow[R];
-  int64_t moff[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, d.N - 1);  // rows past N re-read row N-1 and are never stored
-    wrow[r] = d.qweight + row * words_per_row;
-    moff[r] = static_cast<int64_t>(row) * d.n_groups;
-  }
+// Where block-tile `bt` of the launch sits, as seen by one wave. All fields
+// are wave-uniform. The issue/load/math helpers below cover the chunks
+// [cb, ce) only up to CMAX 16-byte columns per lane: callers split longer
+// ranges into batches of 64 * CMAX chunks.
+struct TilePos {
+  int p;        // problem
+  int row0;     // first row of this wave's tile
+  int cb, ce;   // chunk range [cb, ce) of this wave (its share of K)
+  int kw, wk;   // this wave's share index and the number of shares
+  bool active;  // the block-tile has a tile for this wave
+};
 
-  h2 pow_scale[F::NCLS];
-#pragma unroll
-  for (int c = 0; c < F::NCLS; ++c)
-    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
-  const h2 ones = splat(static_cast<_Float16>(1.0f));
+__device__ __forceinline__ TilePos locate(const KernelBatch& b, int bt, int wave, int R) {
+  TilePos t;
+  int p = 0;
+  while (p + 1 < b.count && bt >= b.bt_start[p + 1]) ++p;
+  const KernelProblem& d = b.p[p];
+  t.p = p;
+  t.wk = d.wk;
+  const int slot = wave / d.wk;
+  t.kw = wave - slot * d.wk;
+  const int tile = (bt - b.bt_start[p]) * (kWavesPerBlock / d.wk) + slot;
+  t.active = tile < d.tiles;
+  t.row0 = tile * R;
+  const int per_wave = (d.n_chunks + d.wk - 1) / d.wk;
+  t.cb = t.kw * per_wave;
+  t.ce = min(d.n_chunks, t.cb + per_wave);
+  return t;
+}
 
-  for (int c0 = cb + lane; c0 < ce; c0 += 64 * CMAX) {
-    // ---- issue every load of the batch
-    u32x4 wv[CMAX][R];
-    uint16_t sraw[CMAX][R], zraw[CMAX][R];
-    h2 xq[MT == 1 ? CMAX : 1][MT == 1 ? 4 : 1][F::PAIRS];
-#pragma unroll
-    for (int t = 0; t < CMAX; ++t) {
-      const int c = c0 + 64 * t;
-      if (c < ce) {
-        const int g = c / d.chunks_per_group;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          // weights are read exactly once: stream them past the caches
-          wv[t][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + 4 * c));
-          sraw[t][r] = d.scales[moff[r] + g];
-          if (!SYM) zraw[t][r] = d.zeros[moff[r] + g];
-        }
-        if constexpr (MT == 1) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) load_x_pairs<BITS, INTER>(d.x + c * F::CPL + j * F::PER, xq[t][j]);
-        }
-      }
-    }
+// The loads of one tile: R rows x CMAX 16-byte chunk columns per lane, plus
+// the rows' fp16 scales (and zeros) of those chunks.
+template <int BITS, int R, int CMAX>
+struct TileLoads {
+  u32x4 w[CMAX][R];
+  uint16_t s[CMAX][R];
+  uint16_t z[CMAX][R];
+};
 
-    // ---- math, one column at a time
+template <int BITS, bool SYM, int R, int CMAX>
+__device__ __forceinline__ void issue_tile(const KernelProblem& d, const TilePos& t, int lane,
+                                           TileLoads<BITS, R, CMAX>& L) {
+  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+  const uint32_t meta_row_bytes = static_cast<uint32_t>(d.n_groups) * 2;
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+  const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row_bytes);
+  const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row_bytes);
 #pragma unroll
-    for (int t = 0; t < CMAX; ++t) {
-      const int c = c0 + 64 * t;
-      if (c < ce) {
-        float sc[R], zf[R];
-        h2 off[R][F::NCLS];
-        bool any_inexact = false;
+  for (int ct = 0; ct < CMAX; ++ct) {
+    const int c = t.cb + lane + 64 * ct;
+    if (c < t.ce) {
+      const uint32_t woff = static_cast<uint32_t>(c) * 16u;
+      const uint32_t moff = static_cast<uint32_t>(c / d.chunks_per_group) * 2u;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          sc[r] = f16_to_f32(sraw[t][r]);
-          zf[r] = SYM ? static_cast<float>(F::BIAS) : f16_to_f32(zraw[t][r]);
-          const bool exact = class_offsets<BITS>(zf[r], off[r]);
-          if (!SYM) {
-            if (exact) zf[r] = 0.f;
-            any_inexact |= !exact;
-          }
-        }
-        // uniform over the lanes of this column: does any need sum(x)?
-        const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
-
-        float acc[R][MT], xsum[MT];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          xsum[m] = 0.f;
-#pragma unroll
-          for (int r = 0; r < R; ++r) acc[r][m] = 0.f;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          h2 xp[MT][F::PAIRS];
-#pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            if (MT == 1 || m < M) {
-              if constexpr (MT == 1) {
-#pragma unroll
-                for (int i = 0; i < F::PAIRS; ++i) xp[m][i] = xq[t][j][i];
-              } else {
-                load_x_pairs<BITS, INTER>(d.x + static_cast<int64_t>(m) * d.K + c * F::CPL + j * F::PER, xp[m]);
-              }
-              if (need_xsum) {
-#pragma unroll
-                for (int i = 0; i < F::PAIRS; ++i) xsum[m] = __builtin_amdgcn_fdot2(xp[m][i], ones, xsum[m], false);
-              }
-            }
-          }
-#pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const uint32_t w = wv[t][r][j];
-            uint32_t mp[F::PAIRS];
-            magic_pairs<BITS>(w, mp);
-            h2 dq2[F::PAIRS];
-#pragma unroll
-            for (int i = 0; i < F::PAIRS; ++i)
-              dq2[i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[r][F::cls(i)]);
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-              if (MT == 1 || m < M) {
-#pragma unroll
-                for (int i = 0; i < F::PAIRS; ++i) acc[r][m] = __builtin_amdgcn_fdot2(dq2[i], xp[m][i], acc[r][m], false);
-              }
-            }
-          }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-#pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            const float u = need_xsum ? __builtin_fmaf(-zf[r], xsum[m], acc[r][m]) : acc[r][m];
-            yacc[r][m] = __builtin_fmaf(sc[r], u, yacc[r][m]);
-          }
-        }
+      for (int r = 0; r < R; ++r) {
+        const uint32_t row = static_cast<uint32_t>(min(t.row0 + r, d.N - 1));  // past N: re-read N-1, never stored
+        // weights are read exactly once: stream them past the caches (slc)
+        L.w[ct][r] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, woff, row * row_bytes, 2);
+        L.s[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(sbuf, moff, row * meta_row_bytes, 0);
+        if (!SYM) L.z[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, row * meta_row_bytes, 0);
       }
     }
   }
 }
 
-// Grouped fused dequant + GEMV. A block (4 waves) belongs to one problem and
-// holds 4/wk tiles of it; a tile is R rows whose K range is split over wk
-// waves meeting in LDS. wk depends only on the problem's own K, so a problem
-// gives bit-identical results whether launched alone or in a group.
+// Activation pairs of CMAX chunk columns of one batch row, in pair order.
+template <int BITS, bool INTER, int CMAX>
+__device__ __forceinline__ void load_x_columns(const KernelProblem& d, const TilePos& t, int lane, int m,
+                                               h2 (&xr)[CMAX][4][Fmt<BITS>::PAIRS]) {
+  using F = Fmt<BITS>;
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(m + 1) * static_cast<uint32_t>(d.K) * 2);
+  const uint32_t mrow = static_cast<uint32_t>(m) * static_cast<uint32_t>(d.K) * 2;
+#pragma unroll
+  for (int ct = 0; ct < CMAX; ++ct) {
+    const int c = t.cb + lane + 64 * ct;
+    if (c < t.ce) {
+      uint32_t xd[F::CPL / 2];
+#pragma unroll
+      for (int q = 0; q < F::CPL / 8; ++q) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xbuf, static_cast<uint32_t>(c) * F::CPL * 2u + 16u * q,
+                                                              mrow, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xd[4 * q + e] = v[e];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xr[ct][j]);
+    }
+  }
+}
+
+// The math of one tile for one batch row m: yacc[r] gets sum over the wave's
+// chunks of scale * sum((q - z) x).
+template <int BITS, bool SYM, bool INTER, int R, int CMAX>
+__device__ __forceinline__ void tile_math(const TilePos& t, int lane, const TileLoads<BITS, R, CMAX>& L,
+                                          const h2 (&xr)[CMAX][4][Fmt<BITS>::PAIRS], uint32_t magic,
+                                          float (&yacc)[R]) {
+  using F = Fmt<BITS>;
+  h2 pow_scale[F::NCLS];
+#pragma unroll
+  for (int c = 0; c < F::NCLS; ++c)
+    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
+  const h2 ones = splat(static_cast<_Float16>(1.0f));
+#pragma unroll
+  for (int ct = 0; ct < CMAX; ++ct) {
+    const int c = t.cb + lane + 64 * ct;
+    if (c < t.ce) {
+      h2 off[R][F::NCLS];
+      bool any_inexact = false;
+#pragma unroll
+      for (int r = 0; r < R; ++r) any_inexact |= !class_offsets<BITS, SYM>(L.z[ct][r], off[r]);
+      // uniform over the active lanes: does any need sum(x)? (out-of-range zero points)
+      const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
+      float acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.f;
+      float xsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (need_xsum) {
+#pragma unroll
+          for (int i = 0; i < F::PAIRS; ++i) xsum = __builtin_amdgcn_fdot2(xr[ct][j][i], ones, xsum, false);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          uint32_t mp[F::PAIRS];
+          magic_pairs<BITS>(L.w[ct][r][j], magic, mp);
+#pragma unroll
+          for (int i = 0; i < F::PAIRS; ++i) {
+            const h2 d2 = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[r][F::cls(i)]);
+            acc[r] = __builtin_amdgcn_fdot2(d2, xr[ct][j][i], acc[r], false);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float u = acc[r];
+        if (need_xsum && (L.z[ct][r] & 0x7FFFu) > 0x6400u)
+          u = __builtin_fmaf(-static_cast<float>(__builtin_bit_cast(_Float16, L.z[ct][r])), xsum, u);
+        yacc[r] = __builtin_fmaf(static_cast<float>(__builtin_bit_cast(_Float16, L.s[ct][r])), u, yacc[r]);
+      }
+    }
+  }
+}
+
+// Reduce the R (x MT) per-lane partial sums of a tile and store y. Block-wide
+// LDS combine when the tile's K is split over wk > 1 waves (`part` is this
+// iteration's half of a double buffer, so one barrier per tile suffices).
+template <int R, int MT>
+__device__ __forceinline__ void finish_tile(const KernelProblem& d, const TilePos& t, int wave, int lane, int M,
+                                            float (&yacc)[R][MT], float (*part)[R * MT]) {
+  wave_sum_lane63<R * MT>(&yacc[0][0]);
+  if (t.wk == 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        if (t.active && lane == 63 && t.row0 + r < d.N && (MT == 1 || m < M))
+          d.y[static_cast<int64_t>(m) * d.N + t.row0 + r] = f32_to_f16_rn(yacc[r][m]);
+  } else {
+    if (lane == 63) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) part[wave][r * MT + m] = yacc[r][m];
+    }
+    __syncthreads();  // all 4 waves of the block run the same block-tile sequence
+    if (t.active && t.kw == 0 && lane < R * MT) {
+      float v = 0.f;
+      for (int j = 0; j < t.wk; ++j) v += part[wave + j][lane];
+      const int r = lane / MT, m = lane - (lane / MT) * MT;
+      if (t.row0 + r < d.N && m < M) d.y[static_cast<int64_t>(m) * d.N + t.row0 + r] = f32_to_f16_rn(v);
+    }
+  }
+}
+
+// Persistent blocks walk the block-tiles bt = blockIdx.x + k * gridDim.x (the
+// grid is sized to the co-resident blocks). Each block-tile gives each wave
+// one tile (R rows x its share of K): every weight/scale/zero load of that
+// tile is issued before its math, and the activations of the wave's chunk
+// columns are gathered per batch row; latency is hidden by the other
+// resident waves.
 template <int BITS, bool SYM, bool INTER, int MT, int R, int CMAX>
 __global__ void __launch_bounds__(kGemvThreads)
-gemv_batched_kernel(const KernelBatch b) {
-  const int wave = threadIdx.x >> 6;
+gemv_kernel(const KernelBatch b) {
+  using F = Fmt<BITS>;
+  // wave-uniform by construction; readfirstlane lets the compiler keep every
+  // derived offset in SGPRs (buffer-load soffset) instead of looping
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
-  int p = 0;
-  while (p + 1 < b.count && static_cast<int>(blockIdx.x) >= b.block_start[p + 1]) ++p;
-  const KernelProblem& d = b.p[p];
-  const int wk = d.wk;
-  const int slot = wave / wk;
-  const int kw = wave - slot * wk;
-  const int tile = (static_cast<int>(blockIdx.x) - b.block_start[p]) * (kWavesPerBlock / wk) + slot;
-  const bool active = tile < d.tiles;
-  const int row0 = tile * R;
-
-  float yacc[R][MT];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int m = 0; m < MT; ++m) yacc[r][m] = 0.f;
-
-  if (active) {
-    const int per_wave = (d.n_chunks + wk - 1) / wk;
-    const int cb = kw * per_wave;
-    const int ce = min(d.n_chunks, cb + per_wave);
-    gemv_tile<BITS, SYM, INTER, MT, R, CMAX>(d, b.M, row0, cb, ce, lane, yacc);
-  }
-
-  if (wk == 1) {
-    // the wave owns the whole row: lane 63 stores
+  __shared__ float part[2][kWavesPerBlock][R * MT];
+  const uint32_t magic = magic_vgpr();
+  const int total = b.bt_start[b.count];
+  int phase = 0;
+  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
+    const TilePos t = locate(b, bt, wave, R);
+    const KernelProblem& d = b.p[t.p];
+    float yacc[R][MT];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const float v = wave_sum_lane63(yacc[r][m]);
-        if (active && lane == 63 && row0 + r < d.N && (MT == 1 || m < b.M))
-          d.y[static_cast<int64_t>(m) * d.N + row0 + r] = f32_to_f16_rn(v);
-      }
-  } else {
-    __shared__ float partial[kWavesPerBlock][R * MT];
+      for (int m = 0; m < MT; ++m) yacc[r][m] = 0.f;
+    if (t.active) {
+      // the wave's share of K in batches of 64 * CMAX chunks (one 16-byte
+      // column per lane per batch and CMAX)
+      for (int cbase = t.cb; cbase < t.ce; cbase += 64 * CMAX) {
+        TilePos tb = t;
+        tb.cb = cbase;
+        tb.ce = min(t.ce, cbase + 64 * CMAX);
+        TileLoads<BITS, R, CMAX> L;
+        issue_tile<BITS, SYM, R, CMAX>(d, tb, lane, L);
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+        for (int m = 0; m < MT; ++m) {
+          if (m < b.M) {
+            h2 xr[CMAX][4][F::PAIRS];
+            load_x_columns<BITS, INTER, CMAX>(d, tb, lane, m, xr);
+            float acc[R];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const float v = wave_sum_lane63(yacc[r][m]);
-        if (lane == 63) partial[wave][r * MT + m] = v;
+            for (int r = 0; r < R; ++r) acc[r] = 0.f;
+            tile_math<BITS, SYM, INTER, R, CMAX>(tb, lane, L, xr, magic, acc);
+#pragma unroll
+            for (int r = 0; r < R; ++r) yacc[r][m] += acc[r];
+          }
+        }
       }
-    __syncthreads();  // every wave of the block reaches this (no early exit above)
-    if (active && kw == 0 && lane < R * MT) {
-      float v = 0.f;
-      for (int j = 0; j < wk; ++j) v += partial[wave + j][lane];
-      const int r = lane / MT, m = lane - (lane / MT) * MT;
-      if (row0 + r < d.N && m < b.M) d.y[static_cast<int64_t>(m) * d.N + row0 + r] = f32_to_f16_rn(v);
     }
+    finish_tile<R, MT>(d, t, wave, lane, b.M, yacc, part[phase]);
+    // the LDS half flips only on tiles that used it (those end with a block
+    // barrier), so a half is rewritten only after every wave has passed the
+    // barrier that follows its last read
+    if (t.wk > 1) phase ^= 1;
   }
 }
 
@@ -476,12 +547,16 @@ int64_t elementwise_blocks(int64_t items) {
 
 // Launch geometry of a grouped GEMV:
 //   wk   per problem, waves per tile along K: the fewest of {1, 2, 4} that
-//        leave each lane at most CMAX 16-byte columns of its row (one batch of
-//        loads); it depends on the problem's K alone;
-//   R    rows per tile, shared by the launch: 4 (activations reused 4x) unless
-//        that leaves fewer than two waves per SIMD on the 1024 SIMDs of an
-//        MI355X, then 2 or 1. R does not change any row's arithmetic.
-constexpr int kCmax = 2;
+//        leave each lane at most CMAX 16-byte columns of its row; rows longer
+//        than 4 * 64 * CMAX chunks take several column batches. It depends on
+//        the problem's K alone, so results do not depend on the grouping.
+//   R    rows per tile, shared by the launch: for M = 1, 4 (activation pairs
+//        reused 4x, one DPP reduction chain per 4 rows) unless that leaves
+//        fewer than two waves per SIMD, then 2 or 1; for M > 1, 1. R does not
+//        change any row's arithmetic.
+//   grid persistent: the co-resident blocks of the kernel (occupancy query,
+//        cached per instance), capped by the number of block-tiles.
+constexpr int kCmax = 1;
 
 int waves_per_tile(int64_t K, int bits) {
   const int64_t chunks = K / (128 / bits);
@@ -492,7 +567,7 @@ int waves_per_tile(int64_t K, int bits) {
 
 int rows_per_tile(const GemvOperand* ops, int count, int64_t M, int bits) {
   if (M > 1) return 1;
-  constexpr int64_t kTargetWaves = 2048;
+  constexpr int64_t kTargetWaves = 2048;  // two per SIMD on the 1024 SIMDs of an MI355X
   int R = 4;
   for (; R > 1; R /= 2) {
     int64_t waves = 0;
@@ -504,18 +579,34 @@ int rows_per_tile(const GemvOperand* ops, int count, int64_t M, int bits) {
 
 thread_local hipEvent_t t_start_event = nullptr, t_stop_event = nullptr;
 
-template <int BITS, bool SYM, bool INTER, int MT, int R>
-hipError_t launch_batch_t(const KernelBatch& kb, hipStream_t stream) {
-  const int blocks = kb.block_start[kb.count];
+template <typename Kernel>
+hipError_t launch_kernel(Kernel kernel, int blocks, const KernelBatch& kb, hipStream_t stream) {
   if (t_start_event && t_stop_event) {
-    hipExtLaunchKernelGGL((gemv_batched_kernel<BITS, SYM, INTER, MT, R, kCmax>), dim3(blocks), dim3(kGemvThreads),
-                          0, stream, t_start_event, t_stop_event, 0, kb);
+    hipExtLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), 0, stream, t_start_event, t_stop_event, 0, kb);
     t_start_event = t_stop_event = nullptr;
   } else {
-    hipLaunchKernelGGL((gemv_batched_kernel<BITS, SYM, INTER, MT, R, kCmax>), dim3(blocks), dim3(kGemvThreads), 0,
-                       stream, kb);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), 0, stream, kb);
   }
   return hipGetLastError();
+}
+
+// Co-resident blocks of a kernel instance on the current device (queried once
+// per instance; the engine targets a single device model, the MI355X).
+template <typename Kernel>
+int resident_blocks(Kernel kernel) {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGemvThreads, 0) != hipSuccess || cus <= 0 ||
+        per_cu <= 0) {
+      (void)hipGetLastError();
+      return 512;
+    }
+    cached = cus * per_cu;
+  }
+  return cached;
 }
 
 template <int BITS, bool SYM, bool INTER, int MT, int R>
@@ -524,7 +615,7 @@ hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream
   KernelBatch kb{};
   kb.count = count;
   kb.M = static_cast<int>(M);
-  int blocks = 0;
+  int bts = 0;
   for (int i = 0; i < count; ++i) {
     const GemvOperand& o = ops[i];
     KernelProblem& k = kb.p[i];
@@ -540,13 +631,14 @@ hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream
     k.n_chunks = static_cast<int>(o.K / CPL);
     k.wk = waves_per_tile(o.K, BITS);
     k.tiles = static_cast<int>((o.N + R - 1) / R);
-    const int tiles_per_block = kWavesPerBlock / k.wk;
-    kb.block_start[i] = blocks;
-    blocks += (k.tiles + tiles_per_block - 1) / tiles_per_block;
+    const int tiles_per_bt = kWavesPerBlock / k.wk;
+    kb.bt_start[i] = bts;
+    bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
   }
-  kb.block_start[count] = blocks;
-  if (blocks == 0) return hipSuccess;
-  return launch_batch_t<BITS, SYM, INTER, MT, R>(kb, stream);
+  kb.bt_start[count] = bts;
+  if (bts == 0) return hipSuccess;
+  auto kernel = gemv_kernel<BITS, SYM, INTER, MT, R, kCmax>;
+  return launch_kernel(kernel, std::min(bts, resident_blocks(kernel)), kb, stream);
 }
 
 template <int BITS, bool SYM, bool INTER>

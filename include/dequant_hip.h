@@ -160,7 +160,7 @@ int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64
  * counterpart): for each problem i, waves_per_tile[i] waves (1, 2 or 4) share
  * one tile along K -- a function of that problem's K only -- and the launch
  * uses *rows_per_tile output rows per tile. The kernel instance is named
- * gemv_batched_kernel<bits, symmetric, interleaved, MT, rows_per_tile, 2> with
+ * gemv_kernel<bits, symmetric, interleaved, MT, rows_per_tile, 1> with
  * MT = 1, 2, 4 or 8 (the smallest >= M). Pure host logic, for profiling and
  * tuning tools. waves_per_tile must hold `count` ints. */
 int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* waves_per_tile,

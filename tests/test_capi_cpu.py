@@ -207,14 +207,15 @@ def test_gemv_plan_geometry():
         assert lib.dq_gemv_plan(arr, len(shapes), m, bits, wk, ctypes.byref(rows)) == 0, lib.dq_last_error()
         return list(wk), rows.value
 
-    # INT4: 32 codes per 16-byte chunk; a wave covers 64 lanes x 2 chunks = 4096 codes
-    assert plan([(14336, 4096)]) == ([1], 4)
-    assert plan([(4096, 14336)]) == ([4], 4)        # 448 chunks -> 4 waves per tile
-    assert plan([(4096, 4096)]) == ([1], 2)         # 4096/4 tiles would leave < 2048 waves
-    assert plan([(1024, 4096)]) == ([1], 1)
-    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([1, 1, 1], 2)
-    assert plan([(4096, 11008)], bits=2) == ([2], 4)  # 172 chunks of 64 codes: 2 waves x 1024 tiles
-    assert plan([(4096, 4096)], m=4) == ([1], 1)
+    # INT4: 32 codes per 16-byte chunk; one 64-lane column of a wave covers 2048 codes.
+    # M = 1 tiles hold 4 rows unless that leaves < 2048 waves, then 2 or 1.
+    assert plan([(14336, 4096)]) == ([2], 4)
+    assert plan([(4096, 14336)]) == ([4], 4)        # 448 chunks -> 4 waves per tile, 2 column batches
+    assert plan([(4096, 4096)]) == ([2], 4)
+    assert plan([(1024, 4096)]) == ([2], 1)
+    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4)
+    assert plan([(4096, 11008)], bits=2) == ([4], 4)  # 172 chunks of 64 codes -> 4 waves per tile
+    assert plan([(4096, 4096)], m=4) == ([2], 1)
     arr = (_native.DqGemvProblem * 1)()
     arr[0].N, arr[0].K = 8, 100
     wk, rows = (ctypes.c_int * 1)(), ctypes.c_int()
