@@ -120,12 +120,14 @@ class Engine:
         for i, (x, p) in enumerate(zip(xs, pws)):
             arr[i].N, arr[i].K = p.shape
             arr[i].group_size = p.config.effective_group_size(p.shape[1])
-        wk, rows = (ctypes.c_int * n)(), ctypes.c_int()
+        wk, rows, kind = (ctypes.c_int * n)(), ctypes.c_int(), ctypes.c_int()
         cfg = pws[0].config
         m = xs[0].shape[0]
-        st = self.capi.dq_gemv_plan(arr, n, m, cfg.bits, wk, ctypes.byref(rows))
+        st = self.capi.dq_gemv_plan(arr, n, m, cfg.bits, wk, ctypes.byref(rows), ctypes.byref(kind))
         self.native.check(st)
         fmt = f"{cfg.bits}, {str(cfg.symmetric).lower()}, {str(cfg.layout == 'interleaved').lower()}"
+        if kind.value == 1:
+            return f"gemv_mfma_kernel<{fmt}, {rows.value // 16}>", tuple(wk)
         mt = 1 if m == 1 else (2 if m == 2 else (4 if m <= 4 else 8))
         return f"gemv_kernel<{fmt}, {mt}, {rows.value}, 1>", tuple(wk)
 

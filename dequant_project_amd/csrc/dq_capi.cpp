@@ -161,9 +161,21 @@ int check_extent(int64_t N, int64_t K) {
   return DQ_OK;
 }
 
+// The GEMV kernels address every operand with 32-bit buffer offsets and use
+// offsets at or above 2^31 as "out of range": each operand must stay below
+// 2 GiB (a Llama-3-70B down_proj is 0.45 GiB at INT8).
+int check_gemv_bytes(int64_t M, int64_t N, int64_t K, int64_t bits, int64_t group_size) {
+  constexpr int64_t kLimit = int64_t(1) << 31;
+  if (N * K / 8 * bits >= kLimit || N * (K / group_size) * 2 >= kLimit || M * K * 2 >= kLimit)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("GEMV operands of shape [", N, ", ", K, "] (M=", M,
+                                             ") exceed the 2 GiB per-operand limit of the GEMV kernels"));
+  return DQ_OK;
+}
+
 // The scalar contract of one raw-pointer GEMV problem.
 int check_gemv_problem(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales, const uint16_t* zeros,
-                       const uint16_t* y, int64_t N, int64_t K, int64_t bits, int64_t group_size, int symmetric) {
+                       const uint16_t* y, int64_t M, int64_t N, int64_t K, int64_t bits, int64_t group_size,
+                       int symmetric) {
   if (!x || !qweight || !scales || !y)
     return fail(DQ_ERR_INVALID_ARGUMENT, "x, qweight, scales and y must not be NULL");
   if (!aligned16(x)) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
@@ -172,7 +184,8 @@ int check_gemv_problem(const uint16_t* x, const uint32_t* qweight, const uint16_
   if ((st = check_zeros_presence(zeros != nullptr, symmetric != 0))) return st;
   if ((st = check_gemv_group(group_size, bits))) return st;
   if (!aligned16(qweight)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
-  return check_extent(N, K);
+  if ((st = check_extent(N, K))) return st;
+  return check_gemv_bytes(M, N, K, bits, group_size);
 }
 
 int launch_status(hipError_t e) {
@@ -220,7 +233,8 @@ int dq_check_gemv(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor*
   if ((st = check_gemv_group(group_size, bits))) return st;
   // this implementation's own requirements
   if (!aligned16(qweight->data)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
-  return check_extent(qweight->sizes[0], K);
+  if ((st = check_extent(qweight->sizes[0], K))) return st;
+  return check_gemv_bytes(x->sizes[0], qweight->sizes[0], K, bits, group_size);
 }
 
 int dq_check_dequantize(const dq_tensor* qweight, const dq_tensor* scales, const dq_tensor* zeros,
@@ -253,7 +267,7 @@ int dq_gemv(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales, 
   g_error.clear();
   int st = check_m(M);
   if (st) return st;
-  if ((st = check_gemv_problem(x, qweight, scales, zeros, y, N, K, bits, group_size, symmetric))) return st;
+  if ((st = check_gemv_problem(x, qweight, scales, zeros, y, M, N, K, bits, group_size, symmetric))) return st;
   if (N == 0) return DQ_OK;
   const dq::GemvOperand op{x, qweight, scales, zeros, y, N, K, group_size};
   return launch_status(dq::launch_gemv_batch(&op, 1, M, static_cast<int>(bits), symmetric != 0, interleaved != 0,
@@ -272,7 +286,7 @@ int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64
   int live = 0;
   for (int i = 0; i < count; ++i) {
     const dq_gemv_problem& p = problems[i];
-    if ((st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, bits, p.group_size,
+    if ((st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, M, p.N, p.K, bits, p.group_size,
                                  symmetric))) {
       g_error = cat("problem ", i, ": ", g_error);
       return st;
@@ -285,12 +299,13 @@ int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64
 }
 
 int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* waves_per_tile,
-                 int* rows_per_tile) {
+                 int* rows_per_tile, int* kernel_kind) {
   g_error.clear();
   if (count < 1 || count > DQ_MAX_BATCH)
     return fail(DQ_ERR_INVALID_ARGUMENT, cat("count must be in [1, ", DQ_MAX_BATCH, "], got ", count));
-  if (!problems || !waves_per_tile || !rows_per_tile)
-    return fail(DQ_ERR_INVALID_ARGUMENT, "problems, waves_per_tile and rows_per_tile must not be NULL");
+  if (!problems || !waves_per_tile || !rows_per_tile || !kernel_kind)
+    return fail(DQ_ERR_INVALID_ARGUMENT,
+                "problems, waves_per_tile, rows_per_tile and kernel_kind must not be NULL");
   int st = check_m(M);
   if (st) return st;
   if (!(bits == 2 || bits == 4 || bits == 8))
@@ -301,9 +316,12 @@ int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t 
     if (p.K <= 0 || p.K % (128 / bits) != 0 || p.N < 0)
       return fail(DQ_ERR_INVALID_ARGUMENT, cat("problem ", i, ": K=", p.K, " must be a positive multiple of ",
                                                128 / bits, " and N=", p.N, " non-negative"));
+    if (p.group_size <= 0 || p.K % p.group_size != 0 || p.group_size % (128 / bits) != 0)
+      return fail(DQ_ERR_INVALID_ARGUMENT, cat("problem ", i, ": group_size=", p.group_size,
+                                               " must divide K and be a multiple of ", 128 / bits));
     ops[i] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
   }
-  dq::plan_gemv_batch(ops, count, M, static_cast<int>(bits), waves_per_tile, rows_per_tile);
+  dq::plan_gemv_batch(ops, count, M, static_cast<int>(bits), waves_per_tile, rows_per_tile, kernel_kind);
   return DQ_OK;
 }
 

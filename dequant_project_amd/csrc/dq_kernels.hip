@@ -211,7 +211,9 @@ __device__ __forceinline__ void x_pairs_from_dwords(const uint32_t* d, h2* xp) {
   }
 }
 
-// Launch-wide description of up to kMaxBatch problems (passed by value).
+// Launch-wide description of up to kMaxBatch problems (passed by value). The
+// host precomputes every quotient the kernel needs, so tile bookkeeping is
+// shifts and adds.
 struct KernelProblem {
   const uint32_t* qweight;
   const uint16_t* scales;
@@ -221,8 +223,10 @@ struct KernelProblem {
   int N, K;
   int n_groups;          // K / group_size
   int chunks_per_group;  // group_size / (128/BITS)
+  int cpg_shift;         // log2(chunks_per_group) when a power of two, else -1
   int n_chunks;          // K / (128/BITS)
-  int wk;                // waves sharing one tile along K (1, 2 or 4)
+  int lwk;               // log2 of the waves sharing one tile along K (wk = 1, 2 or 4)
+  int per_wave;          // ceil(n_chunks / wk): chunks of one wave's share
   int tiles;             // ceil(N / R)
 };
 
@@ -245,22 +249,36 @@ struct TilePos {
   bool active;  // the block-tile has a tile for this wave
 };
 
-__device__ __forceinline__ TilePos locate(const KernelBatch& b, int bt, int wave, int R) {
+// `p` is the problem of the previous block-tile of this block (block-tiles
+// are visited in increasing order, so the search only moves forward).
+__device__ __forceinline__ TilePos locate(const KernelBatch& b, int bt, int wave, int R, int& p) {
   TilePos t;
-  int p = 0;
   while (p + 1 < b.count && bt >= b.bt_start[p + 1]) ++p;
   const KernelProblem& d = b.p[p];
   t.p = p;
-  t.wk = d.wk;
-  const int slot = wave / d.wk;
-  t.kw = wave - slot * d.wk;
-  const int tile = (bt - b.bt_start[p]) * (kWavesPerBlock / d.wk) + slot;
+  t.wk = 1 << d.lwk;
+  const int slot = wave >> d.lwk;
+  t.kw = wave & (t.wk - 1);
+  const int tile = ((bt - b.bt_start[p]) << (2 - d.lwk)) + slot;  // 4 / wk tiles per block-tile
   t.active = tile < d.tiles;
   t.row0 = tile * R;
-  const int per_wave = (d.n_chunks + d.wk - 1) / d.wk;
-  t.cb = t.kw * per_wave;
-  t.ce = min(d.n_chunks, t.cb + per_wave);
+  t.cb = t.kw * d.per_wave;
+  t.ce = min(d.n_chunks, t.cb + d.per_wave);
   return t;
+}
+
+// Buffer offset of 16-byte column c of a batch, or an out-of-range offset
+// (loads return zeros, nothing is read) for lanes past the wave's share.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+__device__ __forceinline__ uint32_t column_offset(int c, int ce, uint32_t bytes_per_column) {
+  return c < ce ? static_cast<uint32_t>(c) * bytes_per_column : kOutOfRange;
+}
+
+// Group of chunk c: a shift when chunks_per_group is a power of two
+// (including every per-channel K that is one), else a division.
+__device__ __forceinline__ uint32_t group_of(const KernelProblem& d, int c) {
+  if (d.cpg_shift >= 0) return static_cast<uint32_t>(c) >> d.cpg_shift;
+  return static_cast<uint32_t>(c) / static_cast<uint32_t>(d.chunks_per_group);
 }
 
 // The loads of one tile: R rows x CMAX 16-byte chunk columns per lane, plus
@@ -282,18 +300,18 @@ __device__ __forceinline__ void issue_tile(const KernelProblem& d, const TilePos
   const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row_bytes);
 #pragma unroll
   for (int ct = 0; ct < CMAX; ++ct) {
+    // lanes past the share read zeros (weights, scale and zero): their terms
+    // vanish because their activations are zero too
     const int c = t.cb + lane + 64 * ct;
-    if (c < t.ce) {
-      const uint32_t woff = static_cast<uint32_t>(c) * 16u;
-      const uint32_t moff = static_cast<uint32_t>(c / d.chunks_per_group) * 2u;
+    const uint32_t woff = column_offset(c, t.ce, 16u);
+    const uint32_t moff = c < t.ce ? group_of(d, c) * 2u : kOutOfRange;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const uint32_t row = static_cast<uint32_t>(min(t.row0 + r, d.N - 1));  // past N: re-read N-1, never stored
-        // weights are read exactly once: stream them past the caches (slc)
-        L.w[ct][r] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, woff, row * row_bytes, 2);
-        L.s[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(sbuf, moff, row * meta_row_bytes, 0);
-        if (!SYM) L.z[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, row * meta_row_bytes, 0);
-      }
+    for (int r = 0; r < R; ++r) {
+      const uint32_t row = static_cast<uint32_t>(min(t.row0 + r, d.N - 1));  // past N: re-read N-1, never stored
+      // weights are read exactly once: stream them past the caches (slc)
+      L.w[ct][r] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, woff, row * row_bytes, 2);
+      L.s[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(sbuf, moff, row * meta_row_bytes, 0);
+      if (!SYM) L.z[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, row * meta_row_bytes, 0);
     }
   }
 }
@@ -307,19 +325,16 @@ __device__ __forceinline__ void load_x_columns(const KernelProblem& d, const Til
   const uint32_t mrow = static_cast<uint32_t>(m) * static_cast<uint32_t>(d.K) * 2;
 #pragma unroll
   for (int ct = 0; ct < CMAX; ++ct) {
-    const int c = t.cb + lane + 64 * ct;
-    if (c < t.ce) {
-      uint32_t xd[F::CPL / 2];
+    const uint32_t xoff = column_offset(t.cb + lane + 64 * ct, t.ce, F::CPL * 2u);
+    uint32_t xd[F::CPL / 2];
 #pragma unroll
-      for (int q = 0; q < F::CPL / 8; ++q) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xbuf, static_cast<uint32_t>(c) * F::CPL * 2u + 16u * q,
-                                                              mrow, 0);
+    for (int q = 0; q < F::CPL / 8; ++q) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xbuf, xoff + 16u * q, mrow, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xd[4 * q + e] = v[e];
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xr[ct][j]);
+      for (int e = 0; e < 4; ++e) xd[4 * q + e] = v[e];
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xr[ct][j]);
   }
 }
 
@@ -337,8 +352,7 @@ __device__ __forceinline__ void tile_math(const TilePos& t, int lane, const Tile
   const h2 ones = splat(static_cast<_Float16>(1.0f));
 #pragma unroll
   for (int ct = 0; ct < CMAX; ++ct) {
-    const int c = t.cb + lane + 64 * ct;
-    if (c < t.ce) {
+    {  // columns past the share hold zeros and add nothing
       h2 off[R][F::NCLS];
       bool any_inexact = false;
 #pragma unroll
@@ -426,8 +440,9 @@ gemv_kernel(const KernelBatch b) {
   const uint32_t magic = magic_vgpr();
   const int total = b.bt_start[b.count];
   int phase = 0;
+  int p = 0;
   for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
-    const TilePos t = locate(b, bt, wave, R);
+    const TilePos t = locate(b, bt, wave, R, p);
     const KernelProblem& d = b.p[t.p];
     float yacc[R][MT];
 #pragma unroll
@@ -463,6 +478,251 @@ gemv_kernel(const KernelBatch b) {
     // barrier), so a half is rewritten only after every wave has passed the
     // barrier that follows its last read
     if (t.wk > 1) phase ^= 1;
+  }
+}
+
+// ------------------------------------------------------ gemv, 2 <= M <= 8 (MFMA)
+// Batch rows share every weight, so for M > 1 the products go to the matrix
+// cores: v_mfma_f32_16x16x32_f16 with the activations as the A operand
+// (16 x 32: rows m, K) and the exact (q - z) weights as the B operand
+// (32 x 16: K, output columns n). Lane l = (kb = l/16, r = l%16):
+//   A  x[min(r, M-1)][8 codes of chunk 4t + kb]       (8 halves)
+//   B  (q - z) of row n = row0 + 16 rb + r, same 8 codes of chunk 4t + kb
+//   D  lane l holds D[m = 4 kb + i][n = r], i = 0..3
+// so one MFMA reduces 32 codes (4 lanes x 8) of 16 rows for all M rows, and
+// the unpack, the group scale (fp32, per lane: the lane's own row) and the
+// (rare) out-of-range-zero correction are the VALU work. An iteration t covers
+// chunks 4t..4t+3 of each row, i.e. 4 * (128/BITS) codes, which must lie in
+// one group: group_size % (4 * 128/BITS) == 0 (the host checks and otherwise
+// uses gemv_kernel). The loads of iteration t+1 are issued before the math of
+// iteration t (two register sets).
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+struct MfmaProblem {
+  const uint32_t* qweight;
+  const uint16_t* scales;
+  const uint16_t* zeros;
+  const uint16_t* x;
+  uint16_t* y;
+  int N, K;
+  int n_groups;   // K / group_size
+  int ipg;        // iterations per group: group_size / (4 * 128/BITS)
+  int ipg_shift;  // log2(ipg) when a power of two, else -1
+  int n_iters;    // K / (4 * 128/BITS)
+  int lwk;        // log2 of the waves sharing one tile along K
+  int per_wave;   // ceil(n_iters / wk)
+  int tiles;      // ceil(N / (16 * RB))
+};
+
+struct MfmaBatch {
+  MfmaProblem p[kMaxBatch];
+  int bt_start[kMaxBatch + 1];
+  int count;
+  int M;
+};
+
+template <int BITS, int RB>
+struct MfmaLoads {
+  u32x4 w[RB];
+  uint16_t s[RB];
+  uint16_t z[RB];
+  u32x4 x[Fmt<BITS>::CPL / 8];
+};
+
+struct MfmaAddr {
+  __amdgpu_buffer_rsrc_t wbuf, sbuf, zbuf, xbuf;
+  uint32_t wv[4], mv[4];  // per-lane row offsets (weights, scales/zeros)
+  uint32_t xv;            // per-lane activation offset
+};
+
+__device__ __forceinline__ h8 pack8(h2 a, h2 b, h2 c, h2 d) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 lo = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+  const h4 hi = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <int BITS, bool SYM, int RB>
+__device__ __forceinline__ void mfma_issue(const MfmaProblem& d, const MfmaAddr& a, int t, MfmaLoads<BITS, RB>& L) {
+  constexpr int CPL = Fmt<BITS>::CPL;
+  const int g = d.n_groups == 1 ? 0 : (d.ipg_shift >= 0 ? t >> d.ipg_shift : t / d.ipg);
+  const uint32_t wso = static_cast<uint32_t>(t) * 64u;
+  const uint32_t mso = static_cast<uint32_t>(g) * 2u;
+  const uint32_t xso = static_cast<uint32_t>(t) * (4u * CPL * 2u);
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    L.w[rb] = __builtin_amdgcn_raw_buffer_load_b128(a.wbuf, a.wv[rb], wso, 2);
+    L.s[rb] = __builtin_amdgcn_raw_buffer_load_b16(a.sbuf, a.mv[rb], mso, 0);
+    if (!SYM) L.z[rb] = __builtin_amdgcn_raw_buffer_load_b16(a.zbuf, a.mv[rb], mso, 0);
+  }
+#pragma unroll
+  for (int q = 0; q < CPL / 8; ++q) L.x[q] = __builtin_amdgcn_raw_buffer_load_b128(a.xbuf, a.xv + 16u * q, xso, 0);
+}
+
+// One iteration: yacc[rb][i] += scale * sum over the iteration's codes.
+template <int BITS, bool SYM, bool INTER, int RB>
+__device__ __forceinline__ void mfma_math(const MfmaLoads<BITS, RB>& L, uint32_t magic, float (&yacc)[RB][4]) {
+  using F = Fmt<BITS>;
+  constexpr int CPL = F::CPL, NMF = CPL / 8, NP = CPL / 2;
+  uint32_t xd[CPL / 2];
+#pragma unroll
+  for (int q = 0; q < CPL / 8; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xd[4 * q + e] = L.x[q][e];
+  h2 xp[NP];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp + j * F::PAIRS);
+  h8 xa[NMF];
+#pragma unroll
+  for (int f = 0; f < NMF; ++f) xa[f] = pack8(xp[4 * f], xp[4 * f + 1], xp[4 * f + 2], xp[4 * f + 3]);
+  h2 pow_scale[F::NCLS];
+#pragma unroll
+  for (int c = 0; c < F::NCLS; ++c)
+    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
+  h2 off[RB][F::NCLS];
+  bool any_inexact = false;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) any_inexact |= !class_offsets<BITS, SYM>(L.z[rb], off[rb]);
+  // sum(x) per batch row, only when some zero point is outside [-1024, 1024]
+  const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
+  f4 xsum = {0.f, 0.f, 0.f, 0.f};
+  if (need_xsum) {
+    const h2 one = splat(static_cast<_Float16>(1.0f));
+    const h8 ones = pack8(one, one, one, one);
+#pragma unroll
+    for (int f = 0; f < NMF; ++f) xsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[f], ones, xsum, 0, 0, 0);
+  }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    h2 dq2[NP];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t mp[F::PAIRS];
+      magic_pairs<BITS>(L.w[rb][j], magic, mp);
+#pragma unroll
+      for (int i = 0; i < F::PAIRS; ++i)
+        dq2[j * F::PAIRS + i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[rb][F::cls(i)]);
+    }
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int f = 0; f < NMF; ++f)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          xa[f], pack8(dq2[4 * f], dq2[4 * f + 1], dq2[4 * f + 2], dq2[4 * f + 3]), acc, 0, 0, 0);
+    if (need_xsum && (L.z[rb] & 0x7FFFu) > 0x6400u) {
+      const float z = f16_to_f32(L.z[rb]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(-z, xsum[i], acc[i]);
+    }
+    const float s = f16_to_f32(L.s[rb]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) yacc[rb][i] = __builtin_fmaf(s, acc[i], yacc[rb][i]);
+  }
+}
+
+// Persistent blocks walk block-tiles like gemv_kernel; a tile is 16 * RB rows
+// and the wk waves of a tile split its iterations, meeting in LDS.
+template <int BITS, bool SYM, bool INTER, int RB>
+__global__ void __launch_bounds__(kGemvThreads) gemv_mfma_kernel(const MfmaBatch b) {
+  using F = Fmt<BITS>;
+  constexpr int CPL = F::CPL;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, kb = lane >> 4;
+  // partial sums of lanes 0..31 (batch rows 0..7) per wave, double-buffered
+  __shared__ float part[2][kWavesPerBlock * RB * 4 * 32];
+  const uint32_t magic = magic_vgpr();
+  const int total = b.bt_start[b.count];
+  int phase = 0;
+  int p = 0;
+  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
+    while (p + 1 < b.count && bt >= b.bt_start[p + 1]) ++p;
+    const MfmaProblem& d = b.p[p];
+    const int wk = 1 << d.lwk;
+    const int slot = wave >> d.lwk;
+    const int kw = wave & (wk - 1);
+    const int tile = ((bt - b.bt_start[p]) << (2 - d.lwk)) + slot;
+    const bool active = tile < d.tiles;
+    const int row0 = tile * 16 * RB;
+    const int ib = kw * d.per_wave;
+    const int ie = min(d.n_iters, ib + d.per_wave);
+    float yacc[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) yacc[rb][i] = 0.f;
+    if (active && ib < ie) {
+      MfmaAddr a;
+      const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+      const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
+      a.wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+      a.sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row);
+      a.zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row);
+      a.xbuf = buffer_of(d.x, static_cast<uint32_t>(b.M) * static_cast<uint32_t>(d.K) * 2u);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const uint32_t n = static_cast<uint32_t>(min(row0 + 16 * rb + r, d.N - 1));  // past N: re-read, never stored
+        a.wv[rb] = n * row_bytes + 16u * kb;
+        a.mv[rb] = n * meta_row;
+      }
+      a.xv = static_cast<uint32_t>(min(r, b.M - 1)) * static_cast<uint32_t>(d.K) * 2u +
+             static_cast<uint32_t>(kb) * (CPL * 2u);
+      // two register sets: loads of the next iteration fly during this one's math
+      MfmaLoads<BITS, RB> A, B;
+      mfma_issue<BITS, SYM, RB>(d, a, ib, A);
+      int t = ib;
+      while (true) {
+        if (t + 1 >= ie) {
+          mfma_math<BITS, SYM, INTER, RB>(A, magic, yacc);
+          break;
+        }
+        mfma_issue<BITS, SYM, RB>(d, a, t + 1, B);
+        mfma_math<BITS, SYM, INTER, RB>(A, magic, yacc);
+        ++t;
+        if (t + 1 >= ie) {
+          mfma_math<BITS, SYM, INTER, RB>(B, magic, yacc);
+          break;
+        }
+        mfma_issue<BITS, SYM, RB>(d, a, t + 1, A);
+        mfma_math<BITS, SYM, INTER, RB>(B, magic, yacc);
+        ++t;
+      }
+    }
+    // lanes 0..31 hold batch rows m = 4 kb + i (< 8) of column n = row0 + 16 rb + r
+    if (wk == 1) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int n = row0 + 16 * rb + r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * kb + i;
+          if (active && kb < 2 && m < b.M && n < d.N) d.y[static_cast<int64_t>(m) * d.N + n] = f32_to_f16_rn(yacc[rb][i]);
+        }
+      }
+    } else {
+      float* pp = part[phase];
+      if (lane < 32) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pp[((wave * RB + rb) * 4 + i) * 32 + lane] = yacc[rb][i];
+      }
+      __syncthreads();  // all 4 waves of the block run the same block-tile sequence
+      if (active && kw == 0 && lane < 32) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          const int n = row0 + 16 * rb + r;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v = 0.f;
+            for (int j = 0; j < wk; ++j) v += pp[(((wave + j) * RB + rb) * 4 + i) * 32 + lane];
+            const int m = 4 * kb + i;
+            if (m < b.M && n < d.N) d.y[static_cast<int64_t>(m) * d.N + n] = f32_to_f16_rn(v);
+          }
+        }
+      }
+      phase ^= 1;  // same rule as gemv_kernel: only tiles that used the LDS flip it
+    }
   }
 }
 
@@ -545,42 +805,66 @@ int64_t elementwise_blocks(int64_t items) {
   return b < 1 ? 1 : (b > 65536 ? 65536 : b);  // grid-stride loops cover the rest
 }
 
-// Launch geometry of a grouped GEMV:
-//   wk   per problem, waves per tile along K: the fewest of {1, 2, 4} that
-//        leave each lane at most CMAX 16-byte columns of its row; rows longer
-//        than 4 * 64 * CMAX chunks take several column batches. It depends on
-//        the problem's K alone, so results do not depend on the grouping.
-//   R    rows per tile, shared by the launch: for M = 1, 4 (activation pairs
-//        reused 4x, one DPP reduction chain per 4 rows) unless that leaves
-//        fewer than two waves per SIMD, then 2 or 1; for M > 1, 1. R does not
-//        change any row's arithmetic.
+// Launch geometry of a grouped GEMV with M = 1 (the VALU kernel), chosen per
+// launch from the problems' shapes:
+//   R    rows per tile: 8 when the launch has at least kWideTiles tiles of 8
+//        rows (long stacks of projections: the activation pairs are reused 8x
+//        and one DPP reduction chain serves 8 rows), else 4.
+//   wk   waves sharing one tile along K (1, 2 or 4): the smallest that gives
+//        the launch kTargetWaves(bits) waves, capped per problem so that each
+//        wave keeps at least kMinColumns 16-byte columns of its rows. INT8 has
+//        the least VALU work per byte and wants the most waves in flight.
 //   grid persistent: the co-resident blocks of the kernel (occupancy query,
 //        cached per instance), capped by the number of block-tiles.
+// Geometry changes only the order of fp32 additions (split-K partial sums),
+// so a problem's result is deterministic for a given launch but may differ in
+// the last bits between a grouped launch and a single one.
 constexpr int kCmax = 1;
+constexpr int64_t kWideTiles = 6144;
+constexpr int64_t kMinColumns = 40;
 
-int waves_per_tile(int64_t K, int bits) {
-  const int64_t chunks = K / (128 / bits);
-  int wk = 1;
-  while (wk < 4 && (chunks + wk - 1) / wk > 64 * kCmax) wk *= 2;
-  return wk;
+int64_t target_waves(int bits) { return bits == 8 ? 8192 : (bits == 4 ? 6144 : 4096); }
+
+int rows_per_tile(const GemvOperand* ops, int count, int64_t M) {
+  if (M > 1) return 1;
+  int64_t tiles8 = 0;
+  for (int i = 0; i < count; ++i) tiles8 += (ops[i].N + 7) / 8;
+  return tiles8 >= kWideTiles ? 8 : 4;
 }
 
-int rows_per_tile(const GemvOperand* ops, int count, int64_t M, int bits) {
-  if (M > 1) return 1;
-  constexpr int64_t kTargetWaves = 2048;  // two per SIMD on the 1024 SIMDs of an MI355X
-  int R = 4;
-  for (; R > 1; R /= 2) {
+// wk[i] for every problem of the launch (rows per tile R).
+void waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk) {
+  const int64_t target = target_waves(bits);
+  int w = 1;
+  for (; w < 4; w *= 2) {
     int64_t waves = 0;
-    for (int i = 0; i < count; ++i) waves += (ops[i].N + R - 1) / R * waves_per_tile(ops[i].K, bits);
-    if (waves >= kTargetWaves) break;
+    for (int i = 0; i < count; ++i) {
+      const int64_t chunks = ops[i].K / (128 / bits);
+      int wi = 1;
+      while (wi < w && chunks / (2 * wi) >= kMinColumns) wi *= 2;
+      waves += (ops[i].N + R - 1) / R * wi;
+    }
+    if (waves >= target) break;
   }
-  return R;
+  for (int i = 0; i < count; ++i) {
+    const int64_t chunks = ops[i].K / (128 / bits);
+    int wi = 1;
+    while (wi < w && chunks / (2 * wi) >= kMinColumns) wi *= 2;
+    wk[i] = wi;
+  }
+}
+
+int log2_exact(int64_t v) {  // log2 of a power of two, else -1
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return s;
 }
 
 thread_local hipEvent_t t_start_event = nullptr, t_stop_event = nullptr;
 
-template <typename Kernel>
-hipError_t launch_kernel(Kernel kernel, int blocks, const KernelBatch& kb, hipStream_t stream) {
+template <typename Kernel, typename Batch>
+hipError_t launch_kernel(Kernel kernel, int blocks, const Batch& kb, hipStream_t stream) {
   if (t_start_event && t_stop_event) {
     hipExtLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), 0, stream, t_start_event, t_stop_event, 0, kb);
     t_start_event = t_stop_event = nullptr;
@@ -612,6 +896,8 @@ int resident_blocks(Kernel kernel) {
 template <int BITS, bool SYM, bool INTER, int MT, int R>
 hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
   constexpr int CPL = 128 / BITS;
+  int wks[kMaxBatch];
+  waves_per_tile(ops, count, BITS, R, wks);
   KernelBatch kb{};
   kb.count = count;
   kb.M = static_cast<int>(M);
@@ -628,10 +914,13 @@ hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream
     k.K = static_cast<int>(o.K);
     k.n_groups = static_cast<int>(o.K / o.group_size);
     k.chunks_per_group = static_cast<int>(o.group_size / CPL);
+    k.cpg_shift = log2_exact(k.chunks_per_group);
     k.n_chunks = static_cast<int>(o.K / CPL);
-    k.wk = waves_per_tile(o.K, BITS);
+    const int wk = wks[i];
+    k.lwk = log2_exact(wk);
+    k.per_wave = (k.n_chunks + wk - 1) / wk;
     k.tiles = static_cast<int>((o.N + R - 1) / R);
-    const int tiles_per_bt = kWavesPerBlock / k.wk;
+    const int tiles_per_bt = kWavesPerBlock / wk;
     kb.bt_start[i] = bts;
     bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
   }
@@ -641,13 +930,82 @@ hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream
   return launch_kernel(kernel, std::min(bts, resident_blocks(kernel)), kb, stream);
 }
 
+// Geometry of the MFMA kernel (2 <= M <= 8):
+//   RB   16-row blocks per tile: 4 when the launch has at least 400 tiles of
+//        64 rows, 2 when it has at least 800 of 32, else 1 (small launches
+//        need the waves more than the reuse of the activation operand).
+//   wk   per problem, waves sharing a tile along K: the fewest of {1, 2, 4}
+//        that leave each wave at most 8 iterations.
+bool mfma_applies(const GemvOperand* ops, int count, int64_t M, int bits) {
+  if (M < 2) return false;
+  const int64_t span = 4 * (128 / bits);  // codes per iteration
+  for (int i = 0; i < count; ++i)
+    if (ops[i].group_size % span != 0) return false;
+  return true;
+}
+
+int mfma_row_blocks(const GemvOperand* ops, int count) {
+  int64_t t4 = 0, t2 = 0;
+  for (int i = 0; i < count; ++i) {
+    t4 += (ops[i].N + 63) / 64;
+    t2 += (ops[i].N + 31) / 32;
+  }
+  return t4 >= 400 ? 4 : (t2 >= 800 ? 2 : 1);
+}
+
+int mfma_waves_per_tile(int64_t K, int bits) {
+  const int64_t iters = K / (4 * (128 / bits));
+  int wk = 1;
+  while (wk < 4 && (iters + wk - 1) / wk > 8) wk *= 2;
+  return wk;
+}
+
+template <int BITS, bool SYM, bool INTER, int RB>
+hipError_t launch_gemv_mfma(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+  constexpr int SPAN = 4 * (128 / BITS);
+  MfmaBatch mb{};
+  mb.count = count;
+  mb.M = static_cast<int>(M);
+  int bts = 0;
+  for (int i = 0; i < count; ++i) {
+    const GemvOperand& o = ops[i];
+    MfmaProblem& k = mb.p[i];
+    k.qweight = o.qweight;
+    k.scales = o.scales;
+    k.zeros = o.zeros;
+    k.x = o.x;
+    k.y = o.y;
+    k.N = static_cast<int>(o.N);
+    k.K = static_cast<int>(o.K);
+    k.n_groups = static_cast<int>(o.K / o.group_size);
+    k.ipg = static_cast<int>(o.group_size / SPAN);
+    k.ipg_shift = log2_exact(k.ipg);
+    k.n_iters = static_cast<int>(o.K / SPAN);
+    const int wk = mfma_waves_per_tile(o.K, BITS);
+    k.lwk = log2_exact(wk);
+    k.per_wave = (k.n_iters + wk - 1) / wk;
+    k.tiles = static_cast<int>((o.N + 16 * RB - 1) / (16 * RB));
+    const int tiles_per_bt = kWavesPerBlock / wk;
+    mb.bt_start[i] = bts;
+    bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
+  }
+  mb.bt_start[count] = bts;
+  if (bts == 0) return hipSuccess;
+  auto kernel = gemv_mfma_kernel<BITS, SYM, INTER, RB>;
+  return launch_kernel(kernel, std::min(bts, resident_blocks(kernel)), mb, stream);
+}
+
 template <int BITS, bool SYM, bool INTER>
 hipError_t launch_gemv_t(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
   if (M == 1) {
-    const int R = rows_per_tile(ops, count, M, BITS);
-    if (R == 4) return launch_gemv_r<BITS, SYM, INTER, 1, 4>(ops, count, M, stream);
-    if (R == 2) return launch_gemv_r<BITS, SYM, INTER, 1, 2>(ops, count, M, stream);
-    return launch_gemv_r<BITS, SYM, INTER, 1, 1>(ops, count, M, stream);
+    if (rows_per_tile(ops, count, M) == 8) return launch_gemv_r<BITS, SYM, INTER, 1, 8>(ops, count, M, stream);
+    return launch_gemv_r<BITS, SYM, INTER, 1, 4>(ops, count, M, stream);
+  }
+  if (mfma_applies(ops, count, M, BITS)) {
+    const int RB = mfma_row_blocks(ops, count);
+    if (RB == 4) return launch_gemv_mfma<BITS, SYM, INTER, 4>(ops, count, M, stream);
+    if (RB == 2) return launch_gemv_mfma<BITS, SYM, INTER, 2>(ops, count, M, stream);
+    return launch_gemv_mfma<BITS, SYM, INTER, 1>(ops, count, M, stream);
   }
   if (M == 2) return launch_gemv_r<BITS, SYM, INTER, 2, 1>(ops, count, M, stream);
   if (M <= 4) return launch_gemv_r<BITS, SYM, INTER, 4, 1>(ops, count, M, stream);
@@ -692,9 +1050,16 @@ hipError_t launch_unpack_t(const uint32_t* qweight, int32_t* out, int64_t N, int
     default: return hipErrorInvalidValue;                                      \
   }
 
-void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows) {
-  for (int i = 0; i < count; ++i) wk[i] = waves_per_tile(ops[i].K, bits);
-  *rows = rows_per_tile(ops, count, M, bits);
+void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows, int* mfma) {
+  if (mfma_applies(ops, count, M, bits)) {
+    *mfma = 1;
+    *rows = 16 * mfma_row_blocks(ops, count);
+    for (int i = 0; i < count; ++i) wk[i] = mfma_waves_per_tile(ops[i].K, bits);
+    return;
+  }
+  *mfma = 0;
+  *rows = rows_per_tile(ops, count, M);
+  waves_per_tile(ops, count, bits, *rows, wk);
 }
 
 void set_launch_events(hipEvent_t start, hipEvent_t stop) {

@@ -49,9 +49,11 @@ def gemv_grouped(xs, pws):
     """Several y_i = x_i @ W_i^T in ONE kernel launch (no reference counterpart).
 
     All weights must share bits / symmetry / layout and all x_i the same
-    number of rows (at most MAX_M); up to 16 problems. Results are bit-identical
-    to calling gemv() per problem. This is the grouped decode launch: q|k|v
-    (same x) or gate|up of a Llama layer.
+    number of rows (at most MAX_M); up to 16 problems. Results match calling
+    gemv() per problem up to fp32 rounding of the split-K partial sums (the
+    launch geometry depends on the whole group) and are deterministic for a
+    given group. This is the grouped decode launch: q|k|v (same x) or gate|up
+    of a Llama layer.
     """
     if not pws:
         return []

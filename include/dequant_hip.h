@@ -124,7 +124,8 @@ int dq_check_unpack(const dq_tensor* qweight, int64_t bits, int64_t K);
  *   zeros    fp16 [N, K/group_size] if !symmetric, else NULL
  *   y        fp16 [M, N] output (written, never read)
  * group_size must divide K and be a multiple of 128/bits codes (one 16-byte
- * load), which excludes INT2 with group_size 32 (dequant_gemv.cu:357-361). */
+ * load), which excludes INT2 with group_size 32 (dequant_gemv.cu:357-361).
+ * Each operand (qweight, scales/zeros, x) must be smaller than 2 GiB. */
 int dq_gemv(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
             const uint16_t* zeros, uint16_t* y, int64_t M, int64_t N, int64_t K,
             int64_t bits, int64_t group_size, int symmetric, int interleaved,
@@ -149,22 +150,29 @@ typedef struct dq_gemv_problem {
  * share M and the format (bits, symmetric, interleaved) in ONE kernel launch,
  * e.g. q|k|v or gate|up of a decoder layer, whose inputs coincide, or the
  * projections of several layers. Each problem obeys the rules of dq_gemv;
- * results equal per-problem dq_gemv calls bit for bit. `problems` is a host
- * array read during the call. No reference counterpart: the reference launches
+ * results match per-problem dq_gemv calls to within fp32 rounding of the
+ * split-K partial sums (see dq_gemv_plan). `problems` is a host array read
+ * during the call. No reference counterpart: the reference launches
  * one kernel per linear (dequant/quant_linear.py:72-82); this is the grouped
  * launch its decode path would use to avoid per-launch overhead. */
 int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
                     int interleaved, dq_stream_t stream);
 
 /* Geometry the launch of these problems would use (no reference
- * counterpart): for each problem i, waves_per_tile[i] waves (1, 2 or 4) share
- * one tile along K -- a function of that problem's K only -- and the launch
- * uses *rows_per_tile output rows per tile. The kernel instance is named
- * gemv_kernel<bits, symmetric, interleaved, MT, rows_per_tile, 1> with
- * MT = 1, 2, 4 or 8 (the smallest >= M). Pure host logic, for profiling and
- * tuning tools. waves_per_tile must hold `count` ints. */
+ * counterpart), for profiling and tuning tools; pure host logic. For each
+ * problem i, waves_per_tile[i] waves (1, 2 or 4) share one tile along K;
+ * the launch uses *rows_per_tile output rows per tile and the kernel
+ *   *kernel_kind == 0: gemv_kernel<bits, symmetric, interleaved, MT,
+ *                      rows_per_tile, 1> (VALU dot products; MT = 1, 2, 4
+ *                      or 8, the smallest >= M), or
+ *   *kernel_kind == 1: gemv_mfma_kernel<bits, symmetric, interleaved,
+ *                      rows_per_tile / 16> (matrix cores; 2 <= M <= 8 when
+ *                      every group_size is a multiple of 4 * 128/bits).
+ * The geometry is chosen per launch, so a problem's result is deterministic
+ * for a given launch but may differ in the last bits between a grouped launch
+ * and a single one. waves_per_tile must hold `count` ints. */
 int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* waves_per_tile,
-                 int* rows_per_tile);
+                 int* rows_per_tile, int* kernel_kind);
 
 /* Profiling hook (no reference counterpart; the reference profiles with
  * Nsight, scripts/bench_dequant_kernel.py:205-229): when both are non-NULL

@@ -196,31 +196,47 @@ def test_torch_binding_rejects_cpu_tensors_with_reference_messages():
 
 
 def test_gemv_plan_geometry():
-    """dq_gemv_plan (host logic): waves per tile from K alone, rows per tile from the total work."""
+    """dq_gemv_plan (host logic): launch geometry chosen per launch from the problems' shapes."""
     lib = _native.capi()
 
-    def plan(shapes, m=1, bits=4):
+    def plan(shapes, m=1, bits=4, gs=128):
         arr = (_native.DqGemvProblem * len(shapes))()
         for i, (n, k) in enumerate(shapes):
-            arr[i].N, arr[i].K, arr[i].group_size = n, k, 128
-        wk, rows = (ctypes.c_int * len(shapes))(), ctypes.c_int()
-        assert lib.dq_gemv_plan(arr, len(shapes), m, bits, wk, ctypes.byref(rows)) == 0, lib.dq_last_error()
-        return list(wk), rows.value
+            arr[i].N, arr[i].K, arr[i].group_size = n, k, gs or k
+        wk, rows, kind = (ctypes.c_int * len(shapes))(), ctypes.c_int(), ctypes.c_int()
+        st = lib.dq_gemv_plan(arr, len(shapes), m, bits, wk, ctypes.byref(rows), ctypes.byref(kind))
+        assert st == 0, lib.dq_last_error()
+        return list(wk), rows.value, kind.value
 
-    # INT4: 32 codes per 16-byte chunk; one 64-lane column of a wave covers 2048 codes.
-    # M = 1 tiles hold 4 rows unless that leaves < 2048 waves, then 2 or 1.
-    assert plan([(14336, 4096)]) == ([2], 4)
-    assert plan([(4096, 14336)]) == ([4], 4)        # 448 chunks -> 4 waves per tile, 2 column batches
-    assert plan([(4096, 4096)]) == ([2], 4)
-    assert plan([(1024, 4096)]) == ([2], 1)
-    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4)
-    assert plan([(4096, 11008)], bits=2) == ([4], 4)  # 172 chunks of 64 codes -> 4 waves per tile
-    assert plan([(4096, 4096)], m=4) == ([2], 1)
+    # M = 1, VALU kernel. INT4: 32 codes per 16-byte column. Rows per tile: 8 for
+    # launches with >= 6144 tiles of 8 rows, else 4. wk: smallest of 1, 2, 4 giving
+    # the launch 6144 waves (INT4), capped so each wave keeps >= 40 columns.
+    assert plan([(14336, 4096)]) == ([2], 4, 0)
+    assert plan([(14336, 4096)] * 2) == ([1, 1], 4, 0)          # gate | up: 7168 waves already
+    assert plan([(4096, 14336)]) == ([4], 4, 0)                 # 448 columns: 112 per wave
+    assert plan([(4096, 4096)]) == ([2], 4, 0)                  # 128 columns: 4 waves would leave 32
+    assert plan([(1024, 4096)]) == ([2], 4, 0)
+    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 0)
+    assert plan([(14336, 4096)] * 16) == ([1] * 16, 8, 0)       # a stack of projections: 8-row tiles
+    assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 0)
+    assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 0)  # 172 columns of 64 codes, 43 per wave
+    assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 0)  # INT8 wants 8192 waves
+    # 2 <= M <= 8: the MFMA kernel when every group spans whole iterations of
+    # 4 * 128/bits codes; 16-row blocks per tile from the launch size, wk from K.
+    assert plan([(4096, 4096)], m=4) == ([4], 16, 1)
+    assert plan([(14336, 4096)] * 2, m=8) == ([4, 4], 64, 1)
+    assert plan([(11008, 4096)], m=4, bits=8, gs=None) == ([4], 16, 1)
+    assert plan([(4096, 11008)], m=4, bits=2, gs=64) == ([1], 1, 0)   # INT2 g64: VALU kernel
+    assert plan([(4096, 4096)], m=2, gs=64) == ([2], 1, 0)             # INT4 g64: VALU kernel
     arr = (_native.DqGemvProblem * 1)()
-    arr[0].N, arr[0].K = 8, 100
-    wk, rows = (ctypes.c_int * 1)(), ctypes.c_int()
-    assert lib.dq_gemv_plan(arr, 1, 1, 4, wk, ctypes.byref(rows)) == 1
+    arr[0].N, arr[0].K, arr[0].group_size = 8, 100, 100
+    wk, rows, kind = (ctypes.c_int * 1)(), ctypes.c_int(), ctypes.c_int()
+    assert lib.dq_gemv_plan(arr, 1, 1, 4, wk, ctypes.byref(rows), ctypes.byref(kind)) == 1
     assert b"must be a positive multiple of 32" in lib.dq_last_error()
+    arr[0].K, arr[0].group_size = 128, 48
+    assert lib.dq_gemv_plan(arr, 1, 1, 4, wk, ctypes.byref(rows), ctypes.byref(kind)) == 1
+    assert b"group_size=48 must divide K" in lib.dq_last_error()
+    assert lib.dq_gemv_plan(arr, 1, 1, 4, wk, ctypes.byref(rows), None) == 1
 
 
 def test_gemv_batched_validation():
