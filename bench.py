@@ -134,10 +134,10 @@ class Engine:
         return f"gemv_kernel<{fmt}, {mt}, {rows.value}, 1>", tuple(wk)
 
 
-def build_stack(torch, layers, seed=20251201):
+def build_stack(torch, layers, seed=20251201, cfg=None):
     from dequant_project_amd.packer import QuantConfig, quantize_tensor
 
-    cfg = QuantConfig(4, 128, False, "sequential")
+    cfg = cfg or QuantConfig(4, 128, False, "sequential")
     gen = torch.Generator(device="cuda").manual_seed(seed)
     stack = []
     for _ in range(layers):
@@ -399,6 +399,26 @@ def main():
                                                     "copy-calibrated; profiles/)", "kernel": dominant,
                 "bytes_per_launch": bytes_per_launch, "mean_launch_us": mean_us, "launches_per_step": n_dom}
 
+    # the same stack step in the other formats (sustained bandwidth of the
+    # INT8 and INT2 kernels over the Llama-3-8B shapes)
+    other_stacks = {}
+    if not args.no_extra:
+        for key, ocfg in [("INT8 per-channel sym", QuantConfig(8, None, True)),
+                          ("INT2 g64 asym", QuantConfig(2, 64, False))]:
+            _, ostack, oxs = build_stack(torch, args.layers, seed=20251202, cfg=ocfg)
+            torch.cuda.synchronize()
+            launches, step_bytes, ms, per = run_mode(torch, eng, ostack, oxs, "stack", args.steps, args.warmup)
+            inst = kernel_instances(eng, launches)
+            other_stacks[key] = {"launches_per_step": len(launches), "bytes_per_step": step_bytes,
+                                 "ms_per_step": ms, "step_ms": summarize(per),
+                                 "gbs": step_bytes / (ms * 1e-3) / 1e9, "us_per_layer": ms * 1e3 / args.layers,
+                                 "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                                 "kernel_instances": {k: len(v) for k, v in inst.items()}}
+            log(f"stack {key}: {ms:.3f} ms/step  {other_stacks[key]['gbs']:.1f} GB/s  "
+                f"{other_stacks[key]['us_per_layer']:.2f} us/layer  ({len(launches)} launches)")
+            del ostack, oxs, launches
+            torch.cuda.empty_cache()
+
     extra = {}
     if not args.no_extra:
         for name, n, k, c, m in [("C1", 4096, 4096, QuantConfig(4, 128, False), 1),
@@ -432,6 +452,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "modes": modes,
+        "other_format_stacks": other_stacks,
         "single_configs": extra,
     }
     print(json.dumps(line, default=lambda o: sorted(o) if isinstance(o, set) else str(o)), flush=True)
