@@ -1,0 +1,239 @@
+"""QuantLinear, gemv() and quantize_model: the Python layer between the kernels
+and a model (the reference's scripts/test_quant_linear.py, tests A-D, restated).
+
+A bug in the reshapes, the M > 8 fallback, the buffer registration or the module
+surgery gives wrong answers that look like a wrong kernel, so these run the real
+module on the GPU and check it with the reference's elementwise criterion
+(oracle.packer_ref.gemv_criterion, scripts/test_quant_linear.py:85-89):
+
+    |y - ref| <= depth * (2^-11 |ref| + 2^-20 |W| @ |x|)
+
+with ref the product of the SAME dequantized weights, so only arithmetic
+rounding is measured. Which dequantized weight depends on the path
+(scripts/test_quant_linear.py:21-36): the fused GEMV (M <= 8) never stores an
+fp16 weight, so its reference is exact_weight (fp32 (q - z) * s); the M > 8
+fallback really multiplies packer.dequantize's fp16 matrix, so that is its
+reference. The CPU tests check the surgery itself (no kernel runs).
+"""
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from dequant_project_amd import packer
+from dequant_project_amd.packer import QuantConfig, quantize_tensor
+from dequant_project_amd.quant_linear import MAX_M, PROJ, QuantLinear, quantize_model
+from oracle import packer_ref as P
+
+
+# --------------------------------------------------------------- fake Llama
+class _Attn(nn.Module):
+    def __init__(self, h):
+        super().__init__()
+        self.q_proj = nn.Linear(h, h, bias=False)
+        self.k_proj = nn.Linear(h, h, bias=False)
+        self.v_proj = nn.Linear(h, h, bias=False)
+        self.o_proj = nn.Linear(h, h, bias=False)
+
+
+class _Mlp(nn.Module):
+    def __init__(self, h, i):
+        super().__init__()
+        self.gate_proj = nn.Linear(h, i, bias=False)
+        self.up_proj = nn.Linear(h, i, bias=False)
+        self.down_proj = nn.Linear(i, h, bias=False)
+
+
+class _Block(nn.Module):
+    def __init__(self, h, i):
+        super().__init__()
+        self.self_attn = _Attn(h)
+        self.mlp = _Mlp(h, i)
+
+    def forward(self, x):
+        a, f = self.self_attn, self.mlp
+        x = a.o_proj(a.q_proj(x) + a.k_proj(x) + a.v_proj(x))
+        return f.down_proj(f.gate_proj(x) + f.up_proj(x))
+
+
+class FakeLlama(nn.Module):
+    """Llama's module names and no nonlinearity: the same forward over |W| and
+    |x| bounds every magnitude the real forward accumulates (the |W|@|x| term of
+    the criterion for a whole stack), scripts/test_quant_linear.py:191-210."""
+
+    def __init__(self, h=256, i=512, n_blocks=2):
+        super().__init__()
+        self.norm = nn.LayerNorm(h)
+        self.layers = nn.ModuleList(_Block(h, i) for _ in range(n_blocks))
+        self.lm_head = nn.Linear(h, h, bias=False)
+
+    def body(self, h):
+        for blk in self.layers:
+            h = blk(h)
+        return self.lm_head(h)
+
+    def forward(self, x):
+        return self.body(self.norm(x))
+
+
+def _fresh_model(device):
+    torch.manual_seed(0)
+    return FakeLlama().to(device=device, dtype=torch.float16).eval()
+
+
+# ------------------------------------------------------------------- CPU
+def test_quantize_model_surgery_cpu():
+    """scripts/test_quant_linear.py:213-244: 14 projections swapped, the rest untouched."""
+    model = _fresh_model("cpu")
+    n_fp16 = sum(m.weight.numel() * 2 for n, m in model.named_modules()
+                 if isinstance(m, nn.Linear) and n.rsplit(".", 1)[-1] in PROJ)
+    stats = quantize_model(model, QuantConfig(4, 128, False))
+    assert stats["replaced"] == 14
+    assert stats["fp16_bytes"] == n_fp16
+    assert 0 < stats["packed_bytes"] < stats["fp16_bytes"]
+    assert type(model.lm_head) is nn.Linear
+    assert isinstance(model.norm, nn.LayerNorm)
+    swapped = [n for n, m in model.named_modules() if isinstance(m, QuantLinear)]
+    assert len(swapped) == 14 and all(n.rsplit(".", 1)[-1] in PROJ for n in swapped)
+    assert not any(n.rsplit(".", 1)[-1] in PROJ and type(m) is nn.Linear for n, m in model.named_modules())
+
+
+def test_quant_linear_buffers_and_state_dict_cpu():
+    """Only packed buffers are registered (no .weight); the packed bytes match packer.py."""
+    torch.manual_seed(1)
+    lin = nn.Linear(256, 96, bias=True).to(torch.float16)
+    cfg = QuantConfig(4, 64, False, "interleaved")
+    ql = QuantLinear.from_linear(lin, cfg)
+    assert not hasattr(ql, "weight")
+    assert set(ql.state_dict()) == {"qweight", "scales", "zeros", "bias"}
+    pw = quantize_tensor(lin.weight.data, cfg)
+    assert torch.equal(ql.qweight, pw.qweight) and torch.equal(ql.scales, pw.scales)
+    assert torch.equal(ql.zeros, pw.zeros) and torch.equal(ql.bias, lin.bias.data)
+    assert ql._packed().nbytes == P.packed_nbytes(96, 256, P.Config(4, 64, False, "interleaved"))
+    sym = QuantLinear.from_linear(nn.Linear(128, 32, bias=False).to(torch.float16), QuantConfig(8, None, True))
+    assert sym.zeros is None and sym.bias is None
+    assert set(sym.state_dict()) == {"qweight", "scales"}
+    assert MAX_M == 8
+
+
+# ------------------------------------------------------------------- GPU
+def _exact_weight(pw):
+    """fp32 (q - off) * s as a torch tensor on pw's device (oracle.exact_weight)."""
+    cfg = P.Config(pw.config.bits, pw.config.group_size, pw.config.symmetric, pw.config.layout)
+    w = P.exact_weight(pw.qweight.cpu().numpy(), pw.scales.cpu().numpy(),
+                       None if pw.zeros is None else pw.zeros.cpu().numpy(), cfg, pw.shape)
+    return torch.from_numpy(np.asarray(w, dtype=np.float32)).to(pw.qweight.device)
+
+
+def _check(y, ref, absref, depth, label):
+    ok, worst = P.gemv_criterion(y.detach().float().cpu().numpy(), ref.detach().double().cpu().numpy(),
+                                 absref.detach().double().cpu().numpy(), depth)
+    print(f"{label}: worst {worst:.3f}x tol", flush=True)
+    assert ok, f"{label}: elementwise criterion violated, worst {worst:.3f}x tol"
+
+
+@pytest.mark.gpu
+def test_gemv_on_3d_input(torch_gpu):
+    """A (scripts/test_quant_linear.py:108-123): gemv() flattens [2, 3, K] to M = 6."""
+    from dequant_project_amd.quant_linear import gemv
+
+    torch.manual_seed(0)
+    n, k = 3072, 3072
+    w = torch.randn(n, k, dtype=torch.float16, device="cuda") * 0.02
+    pw = quantize_tensor(w, QuantConfig(4, 128, False))
+    x = torch.randn(2, 3, k, dtype=torch.float16, device="cuda")
+    y = gemv(x, pw)
+    assert tuple(y.shape) == (2, 3, n)
+    we = _exact_weight(pw)
+    xf = x.float()
+    _check(y, xf @ we.T, xf.abs() @ we.abs().T, 1, "gemv [2,3,3072] INT4 g128 asym")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(1, 3072), (8, 3072), (9, 3072), (64, 3072), (2, 32, 3072)])
+def test_quant_linear_against_f_linear(torch_gpu, shape):
+    """B (scripts/test_quant_linear.py:126-156): both paths of forward, with bias.
+
+    depth 2: the module rounds y to fp16 and then adds the bias (a second fp16
+    rounding) where the reference fuses the bias and rounds once."""
+    from dequant_project_amd.quant_linear import dequantize_cuda
+
+    torch.manual_seed(0)
+    k, n = 3072, 1024
+    lin = nn.Linear(k, n, bias=True).to("cuda", torch.float16)
+    ql = QuantLinear.from_linear(lin, QuantConfig(4, 128, False))
+    pw = ql._packed()
+    assert torch.equal(dequantize_cuda(pw), packer.dequantize(pw))
+    torch.manual_seed(7)
+    x = torch.randn(*shape, dtype=torch.float16, device="cuda")
+    with torch.no_grad():
+        y = ql(x)
+    assert y.shape == (*shape[:-1], n) and y.dtype == torch.float16
+    m = x.numel() // k
+    w_ref = _exact_weight(pw) if m <= MAX_M else packer.dequantize(pw).float()
+    xf = x.float().reshape(m, k)
+    ref = xf @ w_ref.T + ql.bias.float()
+    absref = xf.abs() @ w_ref.abs().T
+    _check(y.reshape(m, n), ref, absref, 2, f"QuantLinear {shape} M={m} via {'gemv' if m <= MAX_M else 'fallback'}")
+
+
+@pytest.mark.gpu
+def test_quantize_model_forward_matches_fake_quant_model(torch_gpu):
+    """C (scripts/test_quant_linear.py:213-258): the quantized model against the
+    same model with each projection's weight replaced by its dequantized fp16
+    copy; the bound is the per-matmul criterion times the 21 fp16 roundings on
+    the path, over the |W|, |x| forward."""
+    cfg = QuantConfig(4, 128, False)
+    model = _fresh_model("cuda")
+    ref_model = copy.deepcopy(model)
+    for name, mod in ref_model.named_modules():
+        if isinstance(mod, nn.Linear) and name.rsplit(".", 1)[-1] in PROJ:
+            mod.weight.data.copy_(packer.dequantize(quantize_tensor(mod.weight.data, cfg)))
+    abs_model = copy.deepcopy(ref_model).float()
+    for p in abs_model.parameters():
+        p.data.abs_()
+    stats = quantize_model(model, cfg)
+    assert stats["replaced"] == 14
+    torch.manual_seed(3)
+    x = torch.randn(1, 256, dtype=torch.float16, device="cuda")
+    with torch.no_grad():
+        y = model(x)
+        ref = ref_model(x).float()
+        absref = abs_model.body(ref_model.norm(x).float().abs())
+    _check(y, ref, absref, 21, "fake Llama forward")
+
+
+@pytest.mark.gpu
+def test_quant_linear_graph_capture(torch_gpu):
+    """D (scripts/test_quant_linear.py:261-291): forward at M = 1 captured into a
+    graph replays bit-identically to eager, also after the input changes."""
+    torch.manual_seed(0)
+    k, n = 3072, 1024
+    lin = nn.Linear(k, n, bias=True).to("cuda", torch.float16)
+    ql = QuantLinear.from_linear(lin, QuantConfig(4, 128, False))
+    x = torch.randn(1, k, dtype=torch.float16, device="cuda")
+    x2 = torch.randn(1, k, dtype=torch.float16, device="cuda")
+    with torch.no_grad():
+        eager1 = ql(x).clone()
+        eager2 = ql(x2).clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                ql(x)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_y = ql(x)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_y, eager1)
+        x.copy_(x2)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_y, eager2)
