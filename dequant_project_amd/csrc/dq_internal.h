@@ -29,8 +29,10 @@ void set_launch_events(hipEvent_t start, hipEvent_t stop);
 
 // Launch geometry a grouped GEMV would use: waves per tile along K for each
 // problem (wk[0..count-1]), the launch's rows per tile, and which kernel runs:
-// *mfma == 0: gemv_kernel<bits, sym, inter, MT, rows, 1> (VALU dot products);
-// *mfma == 1: gemv_mfma_kernel<bits, sym, inter, rows / 16> (2 <= M <= 8).
+// *mfma == 0: gemv_kernel<bits, sym, inter, MT, rows, 1> (VALU dot products, M > 1);
+// *mfma == 1: gemv_mfma_kernel<bits, sym, inter, rows / 16> (2 <= M <= 8);
+// *mfma == 2: gemv_m1_kernel<bits, sym, inter, rows, false> (M = 1, VALU dots);
+// *mfma == 3: gemv_m1_kernel<bits, sym, inter, rows, true> (M = 1, MFMA dots).
 void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows, int* mfma);
 
 // All problems of one launch share M and the format (bits, symmetry, layout).

@@ -286,8 +286,10 @@ __device__ __forceinline__ uint32_t group_of(const KernelProblem& d, int c) {
 template <int BITS, int R, int CMAX>
 struct TileLoads {
   u32x4 w[CMAX][R];
-  uint16_t s[CMAX][R];
-  uint16_t z[CMAX][R];
+  // fp16 bit patterns, zero-extended: 16-bit elements invite the vectorizer
+  // to pair neighbours into <2 x half> reads, which pins the struct in memory
+  uint32_t s[CMAX][R];
+  uint32_t z[CMAX][R];
 };
 
 template <int BITS, bool SYM, int R, int CMAX>
@@ -311,7 +313,7 @@ __device__ __forceinline__ void issue_tile(const KernelProblem& d, const TilePos
       // weights are read exactly once: stream them past the caches (slc)
       L.w[ct][r] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, woff, row * row_bytes, 2);
       L.s[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(sbuf, moff, row * meta_row_bytes, 0);
-      if (!SYM) L.z[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, row * meta_row_bytes, 0);
+      L.z[ct][r] = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, row * meta_row_bytes, 0);
     }
   }
 }
@@ -356,7 +358,7 @@ __device__ __forceinline__ void tile_math(const TilePos& t, int lane, const Tile
       h2 off[R][F::NCLS];
       bool any_inexact = false;
 #pragma unroll
-      for (int r = 0; r < R; ++r) any_inexact |= !class_offsets<BITS, SYM>(L.z[ct][r], off[r]);
+      for (int r = 0; r < R; ++r) any_inexact |= !class_offsets<BITS, SYM>(static_cast<uint16_t>(L.z[ct][r]), off[r]);
       // uniform over the active lanes: does any need sum(x)? (out-of-range zero points)
       const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
       float acc[R];
@@ -384,8 +386,8 @@ __device__ __forceinline__ void tile_math(const TilePos& t, int lane, const Tile
       for (int r = 0; r < R; ++r) {
         float u = acc[r];
         if (need_xsum && (L.z[ct][r] & 0x7FFFu) > 0x6400u)
-          u = __builtin_fmaf(-static_cast<float>(__builtin_bit_cast(_Float16, L.z[ct][r])), xsum, u);
-        yacc[r] = __builtin_fmaf(static_cast<float>(__builtin_bit_cast(_Float16, L.s[ct][r])), u, yacc[r]);
+          u = __builtin_fmaf(-f16_to_f32(static_cast<uint16_t>(L.z[ct][r])), xsum, u);
+        yacc[r] = __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(L.s[ct][r])), u, yacc[r]);
       }
     }
   }
@@ -422,6 +424,191 @@ __device__ __forceinline__ void finish_tile(const KernelProblem& d, const TilePo
   }
 }
 
+// ------------------------------------------------------------- gemv, M = 1
+// The M = 1 hot path. Same tile walk and loads as gemv_kernel, with the math
+// specialized for one activation row:
+//   * the common case (every zero point of the batch within [-1024, 1024])
+//     and the rare one (some zero point outside it, e.g. heavy outliers with
+//     the packer's unclamped zeros) are separate code paths chosen by a
+//     wave-uniform ballot, so the hot loop carries no sum(x) work and no
+//     per-row selects (folding them in as selects cost ~20% more VALU
+//     instructions and registers);
+//   * MF = false: products and sums with v_dot2_f32_f16 (VALU);
+//     MF = true:  the dot products go to the matrix cores. The 64 lanes form
+//     the 16 blocks of v_mfma_f32_4x4x4_16b_f16, four consecutive chunk
+//     columns of one row each; with A = the lane's own activations and B =
+//     its own exact (q - z) codes, register (lane % 4) of the 4x4 result
+//     holds the lane's own dot product (the diagonal), so the load pattern
+//     stays one contiguous 1 KiB row segment per wave and load.
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ h4 cat2(h2 a, h2 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3); }
+
+// One row's dot product for the M = 1 kernel: sum over the lane's chunk of
+// (q - z) x, with (q - z) exact in fp16. `zh` is the zero point to subtract
+// (0 when the caller subtracts z * sum(x) itself).
+template <int BITS, bool INTER, bool MF>
+__device__ __forceinline__ float row_dot_m1(const u32x4& w, _Float16 zh, const h2 (&xr)[1][4][Fmt<BITS>::PAIRS],
+                                            uint32_t magic, int lane) {
+  using F = Fmt<BITS>;
+  h2 pow_scale[F::NCLS];
+#pragma unroll
+  for (int c = 0; c < F::NCLS; ++c)
+    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
+  // exact (q - z) = magic * 2^-p - (2^(10-p) + z)
+  const h2 zz = splat(zh);
+  h2 off[F::NCLS];
+#pragma unroll
+  for (int c = 0; c < F::NCLS; c += 2) {
+    const _Float16 b0 = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c))));
+    const _Float16 b1 =
+        c + 1 < F::NCLS ? static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c + 1)))) : b0;
+    const h2 both = -(h2{b0, b1} + zz);  // one v_pk_add_f16 for two classes
+    off[c] = splat(both.x);
+    if (c + 1 < F::NCLS) off[c + 1] = splat(both.y);
+  }
+  if constexpr (MF) {
+    f4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t mp[F::PAIRS];
+      magic_pairs<BITS>(w[j], magic, mp);
+      h2 dq[F::PAIRS];
+#pragma unroll
+      for (int i = 0; i < F::PAIRS; ++i)
+        dq[i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]);
+#pragma unroll
+      for (int i = 0; i < F::PAIRS; i += 2)
+        D = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xr[0][j][i], xr[0][j][i + 1]), cat2(dq[i], dq[i + 1]), D, 0, 0,
+                                               0);
+    }
+    const bool s1 = lane & 1, s2 = lane & 2;
+    return s2 ? (s1 ? D[3] : D[2]) : (s1 ? D[1] : D[0]);
+  } else {
+    float v = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t mp[F::PAIRS];
+      magic_pairs<BITS>(w[j], magic, mp);
+#pragma unroll
+      for (int i = 0; i < F::PAIRS; ++i) {
+        const h2 d2 = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]);
+        v = __builtin_amdgcn_fdot2(d2, xr[0][j][i], v, false);
+      }
+    }
+    return v;
+  }
+}
+
+// Common case: every zero point of the batch is within [-1024, 1024].
+template <int BITS, bool SYM, bool INTER, int R, bool MF>
+__device__ __forceinline__ void tile_math_m1(const TileLoads<BITS, R, 1>& L, const h2 (&xr)[1][4][Fmt<BITS>::PAIRS],
+                                             uint32_t magic, int lane, float (&acc)[R]) {
+  using F = Fmt<BITS>;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const _Float16 zh = SYM ? static_cast<_Float16>(static_cast<float>(F::BIAS))
+                            : __builtin_bit_cast(_Float16, static_cast<uint16_t>(L.z[0][r]));
+    const float v = row_dot_m1<BITS, INTER, MF>(L.w[0][r], zh, xr, magic, lane);
+    acc[r] = __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(L.s[0][r])), v, acc[r]);
+  }
+}
+
+// Rare case (asymmetric only): some zero point of the batch is outside
+// [-1024, 1024] (or not finite), where (q - z) is not exact in fp16. Such rows
+// take q exactly and subtract z * sum(x) in fp32. It holds none of the tile's
+// loaded registers: it re-reads each row's weights, scale and zero in a
+// rolled loop, so it adds little to the kernel's register budget; results
+// rotate into acc[] in row order.
+template <int BITS, bool INTER, int R, bool MF>
+__device__ __forceinline__ void tile_math_m1_wide_zeros(const KernelProblem& d, const TilePos& tb, int lane,
+                                                                    const h2 (&xr)[1][4][Fmt<BITS>::PAIRS],
+                                                                    uint32_t magic, float (&acc)[R]) {
+  using F = Fmt<BITS>;
+  float xsum = 0.f;
+  const h2 one = splat(static_cast<_Float16>(1.0f));
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < F::PAIRS; ++i) xsum = __builtin_amdgcn_fdot2(xr[0][j][i], one, xsum, false);
+  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+  const uint32_t meta_row_bytes = static_cast<uint32_t>(d.n_groups) * 2;
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+  const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row_bytes);
+  const __amdgpu_buffer_rsrc_t zbuf = buffer_of(d.zeros, static_cast<uint32_t>(d.N) * meta_row_bytes);
+  const int c = tb.cb + lane;
+  const uint32_t woff = column_offset(c, tb.ce, 16u);
+  const uint32_t moff = c < tb.ce ? group_of(d, c) * 2u : kOutOfRange;
+  float res[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) res[r] = 0.f;
+#pragma unroll 1
+  for (int r = 0; r < R; ++r) {
+    const uint32_t row = static_cast<uint32_t>(min(tb.row0 + r, d.N - 1));
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(wbuf, woff, row * row_bytes, 0);
+    const uint32_t sb = __builtin_amdgcn_raw_buffer_load_b16(sbuf, moff, row * meta_row_bytes, 0);
+    const uint32_t zb = __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, row * meta_row_bytes, 0);
+    const bool inexact = (zb & 0x7FFFu) > 0x6400u;
+    const _Float16 zh = inexact ? static_cast<_Float16>(0.0f) : __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb));
+    float v = row_dot_m1<BITS, INTER, MF>(w, zh, xr, magic, lane);
+    if (inexact) v = __builtin_fmaf(-f16_to_f32(static_cast<uint16_t>(zb)), xsum, v);
+#pragma unroll
+    for (int i = 0; i + 1 < R; ++i) res[i] = res[i + 1];
+    res[R - 1] = f16_to_f32(static_cast<uint16_t>(sb)) * v;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = res[r];
+}
+
+template <int BITS, bool SYM, bool INTER, int R, bool MF>
+__global__ void __launch_bounds__(kGemvThreads)
+gemv_m1_kernel(const KernelBatch b) {
+  using F = Fmt<BITS>;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  __shared__ float part[2][kWavesPerBlock][R];
+  const uint32_t magic = magic_vgpr();
+  const int total = b.bt_start[b.count];
+  int phase = 0;
+  int p = 0;
+  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
+    const TilePos t = locate(b, bt, wave, R, p);
+    const KernelProblem& d = b.p[t.p];
+    float yacc[R][1];
+#pragma unroll
+    for (int r = 0; r < R; ++r) yacc[r][0] = 0.f;
+    if (t.active) {
+      for (int cbase = t.cb; cbase < t.ce; cbase += 64) {
+        TilePos tb = t;
+        tb.cb = cbase;
+        tb.ce = min(t.ce, cbase + 64);
+        TileLoads<BITS, R, 1> L;
+        issue_tile<BITS, SYM, R, 1>(d, tb, lane, L);
+        h2 xr[1][4][F::PAIRS];
+        load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
+        bool bad = false;
+        if constexpr (!SYM) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) bad |= (L.z[0][r] & 0x7FFFu) > 0x6400u;
+        }
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+        if (!SYM && __builtin_amdgcn_ballot_w64(bad) != 0)
+          tile_math_m1_wide_zeros<BITS, INTER, R, MF>(d, tb, lane, xr, magic, acc);
+        else
+          tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr, magic, lane, acc);
+#pragma unroll
+        for (int r = 0; r < R; ++r) yacc[r][0] += acc[r];
+      }
+    }
+    finish_tile<R, 1>(d, t, wave, lane, b.M, yacc, part[phase]);
+    if (t.wk > 1) phase ^= 1;
+  }
+}
+
+// ------------------------------------------------ gemv, general M (fallback)
 // Persistent blocks walk the block-tiles bt = blockIdx.x + k * gridDim.x (the
 // grid is sized to the co-resident blocks). Each block-tile gives each wave
 // one tile (R rows x its share of K): every weight/scale/zero load of that
@@ -497,7 +684,6 @@ gemv_kernel(const KernelBatch b) {
 // uses gemv_kernel). The loads of iteration t+1 are issued before the math of
 // iteration t (two register sets).
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
 
 struct MfmaProblem {
   const uint32_t* qweight;
@@ -525,8 +711,8 @@ struct MfmaBatch {
 template <int BITS, int RB>
 struct MfmaLoads {
   u32x4 w[RB];
-  uint16_t s[RB];
-  uint16_t z[RB];
+  uint32_t s[RB];  // fp16 bit patterns, zero-extended (see TileLoads)
+  uint32_t z[RB];
   u32x4 x[Fmt<BITS>::CPL / 8];
 };
 
@@ -554,7 +740,7 @@ __device__ __forceinline__ void mfma_issue(const MfmaProblem& d, const MfmaAddr&
   for (int rb = 0; rb < RB; ++rb) {
     L.w[rb] = __builtin_amdgcn_raw_buffer_load_b128(a.wbuf, a.wv[rb], wso, 2);
     L.s[rb] = __builtin_amdgcn_raw_buffer_load_b16(a.sbuf, a.mv[rb], mso, 0);
-    if (!SYM) L.z[rb] = __builtin_amdgcn_raw_buffer_load_b16(a.zbuf, a.mv[rb], mso, 0);
+    L.z[rb] = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(a.zbuf, a.mv[rb], mso, 0);
   }
 #pragma unroll
   for (int q = 0; q < CPL / 8; ++q) L.x[q] = __builtin_amdgcn_raw_buffer_load_b128(a.xbuf, a.xv + 16u * q, xso, 0);
@@ -583,7 +769,7 @@ __device__ __forceinline__ void mfma_math(const MfmaLoads<BITS, RB>& L, uint32_t
   h2 off[RB][F::NCLS];
   bool any_inexact = false;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) any_inexact |= !class_offsets<BITS, SYM>(L.z[rb], off[rb]);
+  for (int rb = 0; rb < RB; ++rb) any_inexact |= !class_offsets<BITS, SYM>(static_cast<uint16_t>(L.z[rb]), off[rb]);
   // sum(x) per batch row, only when some zero point is outside [-1024, 1024]
   const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
   f4 xsum = {0.f, 0.f, 0.f, 0.f};
@@ -610,11 +796,11 @@ __device__ __forceinline__ void mfma_math(const MfmaLoads<BITS, RB>& L, uint32_t
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
           xa[f], pack8(dq2[4 * f], dq2[4 * f + 1], dq2[4 * f + 2], dq2[4 * f + 3]), acc, 0, 0, 0);
     if (need_xsum && (L.z[rb] & 0x7FFFu) > 0x6400u) {
-      const float z = f16_to_f32(L.z[rb]);
+      const float z = f16_to_f32(static_cast<uint16_t>(L.z[rb]));
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(-z, xsum[i], acc[i]);
     }
-    const float s = f16_to_f32(L.s[rb]);
+    const float s = f16_to_f32(static_cast<uint16_t>(L.s[rb]));
 #pragma unroll
     for (int i = 0; i < 4; ++i) yacc[rb][i] = __builtin_fmaf(s, acc[i], yacc[rb][i]);
   }
@@ -820,6 +1006,13 @@ int64_t elementwise_blocks(int64_t items) {
 // so a problem's result is deterministic for a given launch but may differ in
 // the last bits between a grouped launch and a single one.
 constexpr int kCmax = 1;
+
+// M = 1 dot products on the matrix cores (gemv_m1_kernel<..., MF = true)?
+// Measured on the Llama-3-8B stack shapes (8-row tiles): INT2 g64 48.3% of
+// peak with MFMA vs 46.1% on the VALU (its 16 codes per word make v_dot2 the
+// largest VALU item); INT4 and INT8 within noise or slower, so they stay on
+// the VALU.
+constexpr bool m1_uses_mfma(int bits) { return bits == 2; }
 constexpr int64_t kWideTiles = 6144;
 constexpr int64_t kMinColumns = 40;
 
@@ -874,16 +1067,18 @@ hipError_t launch_kernel(Kernel kernel, int blocks, const Batch& kb, hipStream_t
   return hipGetLastError();
 }
 
-// Co-resident blocks of a kernel instance on the current device (queried once
-// per instance; the engine targets a single device model, the MI355X).
-template <typename Kernel>
-int resident_blocks(Kernel kernel) {
+// Co-resident blocks of a kernel instance on the current device. Queried once
+// per instance: the cache is keyed by the kernel itself (a template argument),
+// because every instance of one kernel template has the same function type.
+// The engine targets a single device model, the MI355X.
+template <auto Kernel>
+int resident_blocks() {
   static int cached = 0;
   if (cached == 0) {
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGemvThreads, 0) != hipSuccess || cus <= 0 ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, kGemvThreads, 0) != hipSuccess || cus <= 0 ||
         per_cu <= 0) {
       (void)hipGetLastError();
       return 512;
@@ -926,8 +1121,14 @@ hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream
   }
   kb.bt_start[count] = bts;
   if (bts == 0) return hipSuccess;
-  auto kernel = gemv_kernel<BITS, SYM, INTER, MT, R, kCmax>;
-  return launch_kernel(kernel, std::min(bts, resident_blocks(kernel)), kb, stream);
+  if constexpr (MT == 1) {
+    constexpr bool MF = m1_uses_mfma(BITS);
+    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, MF>;
+    return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+  } else {
+    constexpr auto kernel = gemv_kernel<BITS, SYM, INTER, MT, R, kCmax>;
+    return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+  }
 }
 
 // Geometry of the MFMA kernel (2 <= M <= 8):
@@ -991,8 +1192,8 @@ hipError_t launch_gemv_mfma(const GemvOperand* ops, int count, int64_t M, hipStr
   }
   mb.bt_start[count] = bts;
   if (bts == 0) return hipSuccess;
-  auto kernel = gemv_mfma_kernel<BITS, SYM, INTER, RB>;
-  return launch_kernel(kernel, std::min(bts, resident_blocks(kernel)), mb, stream);
+  constexpr auto kernel = gemv_mfma_kernel<BITS, SYM, INTER, RB>;
+  return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), mb, stream);
 }
 
 template <int BITS, bool SYM, bool INTER>
@@ -1057,7 +1258,7 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
     for (int i = 0; i < count; ++i) wk[i] = mfma_waves_per_tile(ops[i].K, bits);
     return;
   }
-  *mfma = 0;
+  *mfma = M == 1 ? (m1_uses_mfma(bits) ? 3 : 2) : 0;
   *rows = rows_per_tile(ops, count, M);
   waves_per_tile(ops, count, bits, *rows, wk);
 }

@@ -163,11 +163,17 @@ int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64
  * problem i, waves_per_tile[i] waves (1, 2 or 4) share one tile along K;
  * the launch uses *rows_per_tile output rows per tile and the kernel
  *   *kernel_kind == 0: gemv_kernel<bits, symmetric, interleaved, MT,
- *                      rows_per_tile, 1> (VALU dot products; MT = 1, 2, 4
- *                      or 8, the smallest >= M), or
+ *                      rows_per_tile, 1> (VALU dot products; 2 <= M <= 8,
+ *                      MT = 2, 4 or 8, the smallest >= M, when
+ *                      gemv_mfma_kernel does not apply),
  *   *kernel_kind == 1: gemv_mfma_kernel<bits, symmetric, interleaved,
  *                      rows_per_tile / 16> (matrix cores; 2 <= M <= 8 when
- *                      every group_size is a multiple of 4 * 128/bits).
+ *                      every group_size is a multiple of 4 * 128/bits),
+ *   *kernel_kind == 2: gemv_m1_kernel<bits, symmetric, interleaved,
+ *                      rows_per_tile, false> (M = 1; VALU dot products), or
+ *   *kernel_kind == 3: gemv_m1_kernel<bits, symmetric, interleaved,
+ *                      rows_per_tile, true> (M = 1; dot products on the
+ *                      matrix cores; used for bits == 2).
  * The geometry is chosen per launch, so a problem's result is deterministic
  * for a given launch but may differ in the last bits between a grouped launch
  * and a single one. waves_per_tile must hold `count` ints. */

@@ -208,19 +208,19 @@ def test_gemv_plan_geometry():
         assert st == 0, lib.dq_last_error()
         return list(wk), rows.value, kind.value
 
-    # M = 1, VALU kernel. INT4: 32 codes per 16-byte column. Rows per tile: 8 for
+    # M = 1: gemv_m1_kernel (kind 2; kind 3 = its MFMA-dot variant, INT2). INT4: 32 codes per 16-byte column. Rows per tile: 8 for
     # launches with >= 6144 tiles of 8 rows, else 4. wk: smallest of 1, 2, 4 giving
     # the launch 6144 waves (INT4), capped so each wave keeps >= 40 columns.
-    assert plan([(14336, 4096)]) == ([2], 4, 0)
-    assert plan([(14336, 4096)] * 2) == ([1, 1], 4, 0)          # gate | up: 7168 waves already
-    assert plan([(4096, 14336)]) == ([4], 4, 0)                 # 448 columns: 112 per wave
-    assert plan([(4096, 4096)]) == ([2], 4, 0)                  # 128 columns: 4 waves would leave 32
-    assert plan([(1024, 4096)]) == ([2], 4, 0)
-    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 0)
-    assert plan([(14336, 4096)] * 16) == ([1] * 16, 8, 0)       # a stack of projections: 8-row tiles
-    assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 0)
-    assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 0)  # 172 columns of 64 codes, 43 per wave
-    assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 0)  # INT8 wants 8192 waves
+    assert plan([(14336, 4096)]) == ([2], 4, 2)
+    assert plan([(14336, 4096)] * 2) == ([1, 1], 4, 2)          # gate | up: 7168 waves already
+    assert plan([(4096, 14336)]) == ([4], 4, 2)                 # 448 columns: 112 per wave
+    assert plan([(4096, 4096)]) == ([2], 4, 2)                  # 128 columns: 4 waves would leave 32
+    assert plan([(1024, 4096)]) == ([2], 4, 2)
+    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 2)
+    assert plan([(14336, 4096)] * 16) == ([1] * 16, 8, 2)       # a stack of projections: 8-row tiles
+    assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 2)
+    assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 3)  # 172 columns of 64 codes, 43 per wave
+    assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 2)  # INT8 wants 8192 waves
     # 2 <= M <= 8: the MFMA kernel when every group spans whole iterations of
     # 4 * 128/bits codes; 16-row blocks per tile from the launch size, wk from K.
     assert plan([(4096, 4096)], m=4) == ([4], 16, 1)

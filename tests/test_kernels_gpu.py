@@ -240,6 +240,30 @@ def test_gemv_skewed_weights_negative_zero_points(torch_gpu):
                    deq_ref=False)
 
 
+def test_gemv_zero_points_beyond_fp16_exact_range(torch_gpu):
+    """Zero points outside [-1024, 1024] (unclamped, packer.py:136-137): (q - z)
+    is then not exact in fp16 and the M = 1 kernel takes its separate path
+    (q exactly, minus z * sum(x) in fp32) for the batches that hold one.
+    Bands of 8 rows of far-offset weights alternate with N(0, 0.02) rows, so
+    tiles mix both kinds; every M = 1 kernel variant (VALU and MFMA dots) is
+    covered."""
+    torch = torch_gpu
+    n, k = 256, 4096
+    # offset per format such that zero = round(-min / scale) lands past -1024
+    for fmt, base in [((4, 128, False, "sequential"), 50.0), ((4, 128, False, "interleaved"), 50.0),
+                      ((2, 64, False, "sequential"), 200.0), ((2, 64, False, "interleaved"), 200.0),
+                      ((8, 128, False, "sequential"), 3.0), ((8, None, False, "sequential"), 3.0)]:
+        w = gauss_weight(n, k, seed=31).astype(np.float32)
+        band = (np.arange(n) // 8) % 2 == 1
+        u = np.random.Generator(np.random.PCG64(32)).random((n, k), dtype=np.float32)
+        w[band] = base + 0.5 * u[band]
+        pw, qw, sc, ze = pack_on_gpu(torch, w.astype(np.float16), *fmt)
+        zf = ze.astype(np.float32)
+        assert (np.abs(zf[band]) > 1024).all() and (np.abs(zf[~band]) <= 1024).all(), fmt
+        check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=33) for m in (1, 8)], f"wide zeros {fmt}",
+                   deq_ref=False)
+
+
 # ------------------------------------------------------- benchmark configs
 def test_config_c1_int4_asym_g128(torch_gpu):
     torch = torch_gpu
