@@ -318,6 +318,33 @@ __device__ __forceinline__ void issue_tile(const KernelProblem& d, const TilePos
   }
 }
 
+// issue_tile for the M = 1 kernel (CMAX = 1): zero points first, then scales,
+// then weights. vmcnt retires in issue order, so the zero-point range check
+// that picks the code path waits only for the small loads, and the math of
+// row r starts as soon as weight row r has arrived.
+template <int BITS, bool SYM, int R>
+__device__ __forceinline__ void issue_tile_m1(const KernelProblem& d, const TilePos& t, int lane,
+                                              TileLoads<BITS, R, 1>& L) {
+  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+  const uint32_t meta_row_bytes = static_cast<uint32_t>(d.n_groups) * 2;
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+  const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row_bytes);
+  const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row_bytes);
+  const int c = t.cb + lane;
+  const uint32_t woff = column_offset(c, t.ce, 16u);
+  const uint32_t moff = c < t.ce ? group_of(d, c) * 2u : kOutOfRange;
+  uint32_t rowv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rowv[r] = static_cast<uint32_t>(min(t.row0 + r, d.N - 1));  // past N: re-read N-1
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    L.z[0][r] = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, rowv[r] * meta_row_bytes, 0);
+#pragma unroll
+  for (int r = 0; r < R; ++r) L.s[0][r] = __builtin_amdgcn_raw_buffer_load_b16(sbuf, moff, rowv[r] * meta_row_bytes, 0);
+#pragma unroll
+  for (int r = 0; r < R; ++r) L.w[0][r] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, woff, rowv[r] * row_bytes, 2);
+}
+
 // Activation pairs of CMAX chunk columns of one batch row, in pair order.
 template <int BITS, bool INTER, int CMAX>
 __device__ __forceinline__ void load_x_columns(const KernelProblem& d, const TilePos& t, int lane, int m,
@@ -515,17 +542,18 @@ __device__ __forceinline__ void tile_math_m1(const TileLoads<BITS, R, 1>& L, con
   }
 }
 
-// Rare case (asymmetric only): some zero point of the batch is outside
+// Rare case (asymmetric only): some zero point of the tile is outside
 // [-1024, 1024] (or not finite), where (q - z) is not exact in fp16. Such rows
-// take q exactly and subtract z * sum(x) in fp32. It holds none of the tile's
-// loaded registers: it re-reads each row's weights, scale and zero in a
-// rolled loop, so it adds little to the kernel's register budget; results
-// rotate into acc[] in row order.
+// take q exactly and subtract z * sum(x) in fp32; one call covers one batch. It holds none of the tile's
+// loaded registers: it re-reads the activations, and each row's weights,
+// scale and zero in a rolled loop, so it adds little to the kernel's register
+// budget; results rotate into acc[] in row order.
 template <int BITS, bool INTER, int R, bool MF>
 __device__ __forceinline__ void tile_math_m1_wide_zeros(const KernelProblem& d, const TilePos& tb, int lane,
-                                                                    const h2 (&xr)[1][4][Fmt<BITS>::PAIRS],
-                                                                    uint32_t magic, float (&acc)[R]) {
+                                                        uint32_t magic, float (&acc)[R]) {
   using F = Fmt<BITS>;
+  h2 xr[1][4][F::PAIRS];
+  load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
   float xsum = 0.f;
   const h2 one = splat(static_cast<_Float16>(1.0f));
 #pragma unroll
@@ -579,28 +607,48 @@ gemv_m1_kernel(const KernelBatch b) {
 #pragma unroll
     for (int r = 0; r < R; ++r) yacc[r][0] = 0.f;
     if (t.active) {
+      // the batch loop is branch-free; a batch with a zero point outside
+      // [-1024, 1024] only sets `wide`, and the tile is then redone below
+      bool wide = false;
       for (int cbase = t.cb; cbase < t.ce; cbase += 64) {
         TilePos tb = t;
         tb.cb = cbase;
         tb.ce = min(t.ce, cbase + 64);
-        TileLoads<BITS, R, 1> L;
-        issue_tile<BITS, SYM, R, 1>(d, tb, lane, L);
+        // activations first: vmcnt retires in issue order and every row's
+        // math needs them, so with them last no row could start before the
+        // whole tile had arrived
         h2 xr[1][4][F::PAIRS];
         load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
-        bool bad = false;
+        TileLoads<BITS, R, 1> L;
+        issue_tile_m1<BITS, SYM, R>(d, tb, lane, L);
+        // keep every load of the batch ahead of its math: left alone, the
+        // scheduler sinks the weight loads into the math to save registers,
+        // leaving one or two rows in flight and the latency exposed per row
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (!SYM) {
 #pragma unroll
-          for (int r = 0; r < R; ++r) bad |= (L.z[0][r] & 0x7FFFu) > 0x6400u;
+          for (int r = 0; r < R; ++r) wide |= (L.z[0][r] & 0x7FFFu) > 0x6400u;
         }
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.f;
-        if (!SYM && __builtin_amdgcn_ballot_w64(bad) != 0)
-          tile_math_m1_wide_zeros<BITS, INTER, R, MF>(d, tb, lane, xr, magic, acc);
-        else
-          tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr, magic, lane, acc);
+        tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr, magic, lane, acc);
 #pragma unroll
         for (int r = 0; r < R; ++r) yacc[r][0] += acc[r];
+      }
+      if (!SYM && __builtin_amdgcn_ballot_w64(wide) != 0) {
+        // rare: recompute the whole tile with z * sum(x) for the wide zero points
+#pragma unroll
+        for (int r = 0; r < R; ++r) yacc[r][0] = 0.f;
+        for (int cbase = t.cb; cbase < t.ce; cbase += 64) {
+          TilePos tb = t;
+          tb.cb = cbase;
+          tb.ce = min(t.ce, cbase + 64);
+          float acc[R];
+          tile_math_m1_wide_zeros<BITS, INTER, R, MF>(d, tb, lane, magic, acc);
+#pragma unroll
+          for (int r = 0; r < R; ++r) yacc[r][0] += acc[r];
+        }
       }
     }
     finish_tile<R, 1>(d, t, wave, lane, b.M, yacc, part[phase]);
