@@ -316,7 +316,7 @@ def single_config(torch, eng, name, n, k, cfg, m, reps=10):
     return name, res
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_kernel_int4_c4_stack_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_m1_kernel_int4_c4_stack_traffic.md")
 
 
 def profiled_traffic(kernel):
