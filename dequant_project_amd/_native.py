@@ -82,10 +82,12 @@ SIGNATURES = {
     "dq_status_name": (ctypes.c_char_p, [_I]),
     "dq_version": (_I, []),
     "dq_check_gemv": (_I, [_T, _T, _T, _T, _I64, _I64, _I]),
+    "dq_check_gemm_small": (_I, [_T, _T, _T, _T, _I64, _I64, _I]),
     "dq_check_dequantize": (_I, [_T, _T, _T, _I64, _I64, _I, _I64]),
     "dq_check_unpack": (_I, [_T, _I64, _I64]),
     "dq_gemv": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _I, _P]),
     "dq_gemv_batched": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, _I, _I, _P]),
+    "dq_gemm_small": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, _I, _I, _P]),
     "dq_gemv_plan": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, ctypes.POINTER(ctypes.c_int),
                           ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
     "dq_set_launch_events": (_I, [_P, _P]),

@@ -150,6 +150,14 @@ int check_m(int64_t M) {
   return DQ_OK;
 }
 
+// dq_gemm_small's batch range (no reference counterpart)
+int check_gemm_m(int64_t M) {
+  if (!(M >= 1 && M <= DQ_MAX_GEMM_M))
+    return fail(DQ_ERR_UNSUPPORTED, cat("gemm_small handles 1 <= M <= ", DQ_MAX_GEMM_M, ", got M=", M,
+                                        "; use the dequantize + F.linear fallback"));
+  return DQ_OK;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Limits of this implementation (no reference counterpart: the reference's
@@ -212,8 +220,15 @@ const char* dq_status_name(int status) {
 
 int dq_version(void) { return 100; }
 
-int dq_check_gemv(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor* scales,
-                  const dq_tensor* zeros, int64_t bits, int64_t group_size, int symmetric) {
+}  // extern "C"
+
+namespace {
+
+// The tensor rules of dq_check_gemv / dq_check_gemm_small; `check_rows` is
+// the batch-range rule of the entry point.
+int check_packed_product(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor* scales,
+                         const dq_tensor* zeros, int64_t bits, int64_t group_size, int symmetric,
+                         int (*check_rows)(int64_t)) {
   g_error.clear();
   if (!x || !qweight || !scales)
     return fail(DQ_ERR_INVALID_ARGUMENT, "x, qweight and scales descriptors must not be NULL");
@@ -222,7 +237,7 @@ int dq_check_gemv(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor*
   if (x->dtype != DQ_DTYPE_FLOAT16) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be float16");
   if (!x->contiguous) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be contiguous");
   if (x->ndim != 2) return fail(DQ_ERR_INVALID_ARGUMENT, cat("x must be 2-D [M, K], got ", x->ndim, "-D"));
-  int st = check_m(x->sizes[0]);
+  int st = check_rows(x->sizes[0]);
   if (st) return st;
   if (!aligned16(x->data)) return fail(DQ_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
   const int64_t K = x->sizes[1];
@@ -235,6 +250,20 @@ int dq_check_gemv(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor*
   if (!aligned16(qweight->data)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
   if ((st = check_extent(qweight->sizes[0], K))) return st;
   return check_gemv_bytes(x->sizes[0], qweight->sizes[0], K, bits, group_size);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dq_check_gemv(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor* scales,
+                  const dq_tensor* zeros, int64_t bits, int64_t group_size, int symmetric) {
+  return check_packed_product(x, qweight, scales, zeros, bits, group_size, symmetric, check_m);
+}
+
+int dq_check_gemm_small(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor* scales,
+                        const dq_tensor* zeros, int64_t bits, int64_t group_size, int symmetric) {
+  return check_packed_product(x, qweight, scales, zeros, bits, group_size, symmetric, check_gemm_m);
 }
 
 int dq_check_dequantize(const dq_tensor* qweight, const dq_tensor* scales, const dq_tensor* zeros,
@@ -295,6 +324,30 @@ int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64
   }
   if (live == 0) return DQ_OK;
   return launch_status(dq::launch_gemv_batch(ops, live, M, static_cast<int>(bits), symmetric != 0,
+                                             interleaved != 0, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
+                  int interleaved, dq_stream_t stream) {
+  g_error.clear();
+  if (count < 1 || count > DQ_MAX_BATCH)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("count must be in [1, ", DQ_MAX_BATCH, "], got ", count));
+  if (!problems) return fail(DQ_ERR_INVALID_ARGUMENT, "problems must not be NULL");
+  int st = check_gemm_m(M);
+  if (st) return st;
+  dq::GemvOperand ops[DQ_MAX_BATCH];
+  int live = 0;
+  for (int i = 0; i < count; ++i) {
+    const dq_gemv_problem& p = problems[i];
+    if ((st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, M, p.N, p.K, bits, p.group_size,
+                                 symmetric))) {
+      g_error = cat("problem ", i, ": ", g_error);
+      return st;
+    }
+    if (p.N > 0) ops[live++] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
+  }
+  if (live == 0) return DQ_OK;
+  return launch_status(dq::launch_gemm_batch(ops, live, M, static_cast<int>(bits), symmetric != 0,
                                              interleaved != 0, reinterpret_cast<hipStream_t>(stream)));
 }
 

@@ -39,6 +39,19 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
 hipError_t launch_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
                              bool interleaved, hipStream_t stream);
 
+// Largest M the small fused GEMM takes (launch_gemm_batch).
+constexpr int kMaxGemmM = 64;
+
+// y = x @ W16^T for 1 <= M <= kMaxGemmM with W16 the fp16 weight that
+// dequantize materializes, built in registers (one pass over the packed
+// bytes, fp32 accumulation on the matrix cores). Same operands as
+// launch_gemv_batch.
+hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
+                             bool interleaved, hipStream_t stream);
+
+// Waves per 16-row tile along K for each problem of a small-GEMM launch.
+void plan_gemm_batch(const GemvOperand* ops, int count, int bits, int* wk);
+
 struct DequantProblem {
   const uint32_t* qweight;
   const uint16_t* scales;

@@ -960,42 +960,259 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_mfma_kernel(const MfmaBatch
   }
 }
 
+// ---------------------------------------------------- small GEMM, M <= 64 (MFMA)
+// y[m, n] = fp16( sum_k x[m, k] * W16[n, k] ) with W16 = fp16((q - z) * s),
+// the fp16 weight packer.dequantize materializes (packer.py:177-189), built
+// in registers: (q - z) exact in fp16 (as in the GEMV kernels) times the fp16
+// scale with one v_pk_mul_f16 is the exact product rounded once to fp16, i.e.
+// the same bits as dequantize's fp32 multiply and RNE store. So this computes
+// the reference's M > 8 path (dequantize, then F.linear over the fp16 weight:
+// quant_linear.py:131-132) in one pass over the packed bytes, with fp32
+// accumulation on the matrix cores; only the summation order differs.
+//
+// v_mfma_f32_16x16x32_f16 with the activations as A (16 batch rows x 32 k)
+// and W16 as B (32 k x 16 output columns), lane l = (kb = l/16, r = l%16):
+//   B  8 weights of row n = row0 + r: fragment f of chunk 4t + kb
+//   A  the matching 8 activations of batch row 16 mb + r
+//   D  lane l holds y[16 mb + 4 kb + i][row0 + r], i = 0..3
+// A tile is 16 rows; an iteration covers chunks 4t..4t+3 of them, and each of
+// the MB activation tiles reuses the iteration's W16 fragments. Zero points
+// outside [-1024, 1024] take W16 from fp32 arithmetic instead (wave-uniform
+// branch, rare).
+struct GemmProblem {
+  const uint32_t* qweight;
+  const uint16_t* scales;
+  const uint16_t* zeros;
+  const uint16_t* x;
+  uint16_t* y;
+  int N, K;
+  int n_groups;   // K / group_size
+  int cpg_shift;  // log2(chunks per group) when a power of two, else -1
+  int cpg;        // chunks per group
+  int n_chunks;   // K / (128/BITS)
+  int n_iters;    // ceil(n_chunks / 4)
+  int lwk;        // log2 of the waves sharing one tile along K
+  int per_wave;   // ceil(n_iters / wk)
+  int tiles;      // ceil(N / 16)
+};
+
+struct GemmBatch {
+  GemmProblem p[kMaxBatch];
+  int bt_start[kMaxBatch + 1];
+  int count;
+  int M;
+};
+
+// W16 fragments of one lane's chunk (CPL codes = CPL/8 fragments of 8).
+template <int BITS, bool SYM, bool WIDE>
+__device__ __forceinline__ void w16_fragments(const u32x4& w, uint32_t sb, uint32_t zb, uint32_t magic,
+                                              h8 (&wf)[Fmt<BITS>::CPL / 8]) {
+  using F = Fmt<BITS>;
+  constexpr int NP = F::CPL / 2;
+  h2 dq[NP];
+  if constexpr (!WIDE) {
+    h2 pow_scale[F::NCLS];
+#pragma unroll
+    for (int c = 0; c < F::NCLS; ++c)
+      pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
+    const _Float16 zh = SYM ? static_cast<_Float16>(static_cast<float>(F::BIAS))
+                            : __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb));
+    const h2 zz = splat(zh);
+    h2 off[F::NCLS];
+#pragma unroll
+    for (int c = 0; c < F::NCLS; c += 2) {
+      const _Float16 b0 = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c))));
+      const _Float16 b1 =
+          c + 1 < F::NCLS ? static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c + 1)))) : b0;
+      const h2 both = -(h2{b0, b1} + zz);
+      off[c] = splat(both.x);
+      if (c + 1 < F::NCLS) off[c + 1] = splat(both.y);
+    }
+    const h2 ss = splat(__builtin_bit_cast(_Float16, static_cast<uint16_t>(sb)));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t mp[F::PAIRS];
+      magic_pairs<BITS>(w[j], magic, mp);
+#pragma unroll
+      for (int i = 0; i < F::PAIRS; ++i)
+        dq[j * F::PAIRS + i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]) * ss;
+    }
+  } else {
+    // fp32 (q - z) * s then fp16 RNE, dequantize_kernel's own arithmetic
+    const float s = f16_to_f32(static_cast<uint16_t>(sb));
+    const float z = SYM ? static_cast<float>(F::BIAS) : f16_to_f32(static_cast<uint16_t>(zb));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < F::PAIRS; ++i) {
+        const float qa = static_cast<float>((w[j] >> (BITS * i)) & ((1u << BITS) - 1u));
+        const float qb = static_cast<float>((w[j] >> (BITS * (i + F::PAIRS))) & ((1u << BITS) - 1u));
+        dq[j * F::PAIRS + i] = h2{static_cast<_Float16>(__fmul_rn(qa - z, s)), static_cast<_Float16>(__fmul_rn(qb - z, s))};
+      }
+    }
+  }
+#pragma unroll
+  for (int f = 0; f < F::CPL / 8; ++f) wf[f] = pack8(dq[4 * f], dq[4 * f + 1], dq[4 * f + 2], dq[4 * f + 3]);
+}
+
+template <int BITS, bool SYM, bool INTER, int MB>
+__global__ void __launch_bounds__(kGemvThreads) gemm_mfma_kernel(const GemmBatch b) {
+  using F = Fmt<BITS>;
+  constexpr int CPL = F::CPL, NF = CPL / 8;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, kb = lane >> 4;
+  __shared__ float part[2][kWavesPerBlock][MB * 4][64];
+  const uint32_t magic = magic_vgpr();
+  const int total = b.bt_start[b.count];
+  int phase = 0;
+  int p = 0;
+  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
+    while (p + 1 < b.count && bt >= b.bt_start[p + 1]) ++p;
+    const GemmProblem& d = b.p[p];
+    const int wk = 1 << d.lwk;
+    const int slot = wave >> d.lwk;
+    const int kw = wave & (wk - 1);
+    const int tile = ((bt - b.bt_start[p]) << (2 - d.lwk)) + slot;
+    const bool active = tile < d.tiles;
+    const int row0 = tile * 16;
+    const int ib = kw * d.per_wave;
+    const int ie = min(d.n_iters, ib + d.per_wave);
+    f4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
+    if (active && ib < ie) {
+      const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+      const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
+      const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+      const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row);
+      const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row);
+      const __amdgpu_buffer_rsrc_t xbuf =
+          buffer_of(d.x, static_cast<uint32_t>(b.M) * static_cast<uint32_t>(d.K) * 2u);
+      const uint32_t n = static_cast<uint32_t>(min(row0 + r, d.N - 1));  // past N: re-read, never stored
+      const uint32_t wrow = n * row_bytes, mrow = n * meta_row;
+      uint32_t xrow[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        xrow[mb] = static_cast<uint32_t>(min(16 * mb + r, b.M - 1)) * static_cast<uint32_t>(d.K) * 2u;
+      for (int t = ib; t < ie; ++t) {
+        const int c = 4 * t + kb;
+        const bool cok = c < d.n_chunks;
+        const uint32_t g = d.n_groups == 1 ? 0u
+                           : (d.cpg_shift >= 0 ? static_cast<uint32_t>(c) >> d.cpg_shift
+                                               : static_cast<uint32_t>(c) / static_cast<uint32_t>(d.cpg));
+        const uint32_t zb = SYM ? 0u
+                                : __builtin_amdgcn_raw_buffer_load_b16(zbuf, cok ? mrow + g * 2u : kOutOfRange, 0, 0);
+        const uint32_t sb = __builtin_amdgcn_raw_buffer_load_b16(sbuf, cok ? mrow + g * 2u : kOutOfRange, 0, 0);
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(
+            wbuf, cok ? wrow + static_cast<uint32_t>(c) * 16u : kOutOfRange, 0, 2);
+        u32x4 xv[MB][CPL / 8];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int q = 0; q < CPL / 8; ++q)
+            xv[mb][q] = __builtin_amdgcn_raw_buffer_load_b128(
+                xbuf, cok ? xrow[mb] + static_cast<uint32_t>(c) * (CPL * 2u) + 16u * q : kOutOfRange, 0, 0);
+        h8 wf[NF];
+        const bool wide = !SYM && (zb & 0x7FFFu) > 0x6400u;
+        if (!SYM && __builtin_amdgcn_ballot_w64(wide) != 0)
+          w16_fragments<BITS, SYM, true>(w, sb, zb, magic, wf);
+        else
+          w16_fragments<BITS, SYM, false>(w, sb, zb, magic, wf);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          uint32_t xd[CPL / 2];
+#pragma unroll
+          for (int q = 0; q < CPL / 8; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xd[4 * q + e] = xv[mb][q][e];
+          h2 xp[CPL / 2];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp + j * F::PAIRS);
+#pragma unroll
+          for (int f = 0; f < NF; ++f)
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                pack8(xp[4 * f], xp[4 * f + 1], xp[4 * f + 2], xp[4 * f + 3]), wf[f], acc[mb], 0, 0, 0);
+        }
+      }
+    }
+    // lane (kb, r) holds y[16 mb + 4 kb + i][row0 + r]
+    const int ncol = row0 + r;
+    if (wk == 1) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 16 * mb + 4 * kb + i;
+          if (active && m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.N + ncol] = f32_to_f16_rn(acc[mb][i]);
+        }
+    } else {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[phase][wave][4 * mb + i][lane] = acc[mb][i];
+      __syncthreads();  // all 4 waves of the block run the same block-tile sequence
+      if (active && kw == 0) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v = 0.f;
+            for (int j = 0; j < wk; ++j) v += part[phase][wave + j][4 * mb + i][lane];
+            const int m = 16 * mb + 4 * kb + i;
+            if (m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.N + ncol] = f32_to_f16_rn(v);
+          }
+      }
+      phase ^= 1;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- dequantize
 constexpr int kElemThreads = 256;
 
+// Rows are walked along the grid's y dimension (a row index is uniform per
+// block: no per-thread division) and a row's 32-bit words along x. A word
+// lies in one group (group_size % (32/BITS) == 0): its group is a shift of
+// the word index when words per group is a power of two (gshift >= 0), 0 for
+// per-channel weights (one group), else a 32-bit division.
 template <int BITS, bool SYM, bool INTER>
 __global__ void __launch_bounds__(kElemThreads)
 dequantize_kernel(const uint32_t* __restrict__ qweight, const uint16_t* __restrict__ scales,
-                  const uint16_t* __restrict__ zeros, uint16_t* __restrict__ out,
-                  int64_t total_words, int K, int group_size) {
+                  const uint16_t* __restrict__ zeros, uint16_t* __restrict__ out, int N, int K, int group_size,
+                  int gshift) {
   using F = Fmt<BITS>;
-  const int64_t words_per_row = K / F::PER;
+  const int wpr = K / F::PER;  // words per row
   const int ng = K / group_size;
-  for (int64_t widx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; widx < total_words;
-       widx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t n = widx / words_per_row;
-    const int k0 = static_cast<int>(widx - n * words_per_row) * F::PER;
-    const int64_t gidx = n * ng + k0 / group_size;  // group_size % PER == 0: one group per word
-    const float s = f16_to_f32(scales[gidx]);
-    const float off = SYM ? static_cast<float>(F::BIAS) : f16_to_f32(zeros[gidx]);
-    const uint32_t w = qweight[widx];
-    uint16_t v[F::PER];
+  const int wpg = group_size / F::PER;
+  for (int n = blockIdx.y; n < N; n += gridDim.y) {
+    const uint32_t* qrow = qweight + static_cast<int64_t>(n) * wpr;
+    const uint16_t* srow = scales + static_cast<int64_t>(n) * ng;
+    const uint16_t* zrow = SYM ? nullptr : zeros + static_cast<int64_t>(n) * ng;
+    uint16_t* orow = out + static_cast<int64_t>(n) * K;
+    for (int w = blockIdx.x * kElemThreads + threadIdx.x; w < wpr; w += gridDim.x * kElemThreads) {
+      const int g = ng == 1 ? 0 : (gshift >= 0 ? (w >> gshift) : w / wpg);
+      const float s = f16_to_f32(srow[g]);
+      const float off = SYM ? static_cast<float>(F::BIAS) : f16_to_f32(zrow[g]);
+      const uint32_t word = qrow[w];
+      uint16_t v[F::PER];
 #pragma unroll
-    for (int sl = 0; sl < F::PER; ++sl) {
-      const float code = static_cast<float>((w >> (BITS * sl)) & ((1u << BITS) - 1u));
-      // (code - off) then a separate fp32 multiply, then fp16 RNE: packer.py:183-189
-      const float d = code - off;
-      v[logical_of_slot<BITS, INTER>(sl)] = f32_to_f16_rn(__fmul_rn(d, s));
-    }
-    uint16_t* o = out + n * K + k0;
-    if constexpr (F::PER == 4) {
-      *reinterpret_cast<uint2*>(o) = make_uint2(v[0] | (uint32_t(v[1]) << 16), v[2] | (uint32_t(v[3]) << 16));
-    } else {
+      for (int sl = 0; sl < F::PER; ++sl) {
+        const float code = static_cast<float>((word >> (BITS * sl)) & ((1u << BITS) - 1u));
+        // (code - off) then a separate fp32 multiply, then fp16 RNE: packer.py:183-189
+        const float d = code - off;
+        v[logical_of_slot<BITS, INTER>(sl)] = f32_to_f16_rn(__fmul_rn(d, s));
+      }
+      uint16_t* o = orow + static_cast<int64_t>(w) * F::PER;
+      if constexpr (F::PER == 4) {
+        *reinterpret_cast<uint2*>(o) = make_uint2(v[0] | (uint32_t(v[1]) << 16), v[2] | (uint32_t(v[3]) << 16));
+      } else {
 #pragma unroll
-      for (int q = 0; q < F::PER / 8; ++q)
-        *reinterpret_cast<uint4*>(o + 8 * q) = make_uint4(
-            v[8 * q + 0] | (uint32_t(v[8 * q + 1]) << 16), v[8 * q + 2] | (uint32_t(v[8 * q + 3]) << 16),
-            v[8 * q + 4] | (uint32_t(v[8 * q + 5]) << 16), v[8 * q + 6] | (uint32_t(v[8 * q + 7]) << 16));
+        for (int q = 0; q < F::PER / 8; ++q)
+          *reinterpret_cast<uint4*>(o + 8 * q) = make_uint4(
+              v[8 * q + 0] | (uint32_t(v[8 * q + 1]) << 16), v[8 * q + 2] | (uint32_t(v[8 * q + 3]) << 16),
+              v[8 * q + 4] | (uint32_t(v[8 * q + 5]) << 16), v[8 * q + 6] | (uint32_t(v[8 * q + 7]) << 16));
+      }
     }
   }
 }
@@ -1244,6 +1461,79 @@ hipError_t launch_gemv_mfma(const GemvOperand* ops, int count, int64_t M, hipStr
   return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), mb, stream);
 }
 
+// Geometry of the small GEMM (8 < M <= 64, or any M <= 64 the caller sends):
+// MB activation tiles of 16 rows; 16-row weight tiles; wk waves per tile
+// along K, the fewest of {1, 2, 4} that give the launch kGemmWaves waves while
+// leaving each wave at least 4 iterations of 4 chunks.
+constexpr int64_t kGemmWaves = 4096;
+
+int gemm_waves_per_tile(const GemvOperand* ops, int count, int bits, int* wk) {
+  const int cpl = 128 / bits;
+  int w = 1;
+  for (; w < 4; w *= 2) {
+    int64_t waves = 0;
+    for (int i = 0; i < count; ++i) {
+      const int64_t iters = (ops[i].K / cpl + 3) / 4;
+      int wi = 1;
+      while (wi < w && iters / (2 * wi) >= 4) wi *= 2;
+      waves += (ops[i].N + 15) / 16 * wi;
+    }
+    if (waves >= kGemmWaves) break;
+  }
+  for (int i = 0; i < count; ++i) {
+    const int64_t iters = (ops[i].K / cpl + 3) / 4;
+    int wi = 1;
+    while (wi < w && iters / (2 * wi) >= 4) wi *= 2;
+    wk[i] = wi;
+  }
+  return w;
+}
+
+template <int BITS, bool SYM, bool INTER, int MB>
+hipError_t launch_gemm_mb(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+  constexpr int CPL = 128 / BITS;
+  int wks[kMaxBatch];
+  gemm_waves_per_tile(ops, count, BITS, wks);
+  GemmBatch gb{};
+  gb.count = count;
+  gb.M = static_cast<int>(M);
+  int bts = 0;
+  for (int i = 0; i < count; ++i) {
+    const GemvOperand& o = ops[i];
+    GemmProblem& k = gb.p[i];
+    k.qweight = o.qweight;
+    k.scales = o.scales;
+    k.zeros = o.zeros;
+    k.x = o.x;
+    k.y = o.y;
+    k.N = static_cast<int>(o.N);
+    k.K = static_cast<int>(o.K);
+    k.n_groups = static_cast<int>(o.K / o.group_size);
+    k.cpg = static_cast<int>(o.group_size / CPL);
+    k.cpg_shift = log2_exact(k.cpg);
+    k.n_chunks = static_cast<int>(o.K / CPL);
+    k.n_iters = (k.n_chunks + 3) / 4;
+    const int wk = wks[i];
+    k.lwk = log2_exact(wk);
+    k.per_wave = (k.n_iters + wk - 1) / wk;
+    k.tiles = static_cast<int>((o.N + 15) / 16);
+    const int tiles_per_bt = kWavesPerBlock / wk;
+    gb.bt_start[i] = bts;
+    bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
+  }
+  gb.bt_start[count] = bts;
+  if (bts == 0) return hipSuccess;
+  constexpr auto kernel = gemm_mfma_kernel<BITS, SYM, INTER, MB>;
+  return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), gb, stream);
+}
+
+template <int BITS, bool SYM, bool INTER>
+hipError_t launch_gemm_t(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+  if (M <= 16) return launch_gemm_mb<BITS, SYM, INTER, 1>(ops, count, M, stream);
+  if (M <= 32) return launch_gemm_mb<BITS, SYM, INTER, 2>(ops, count, M, stream);
+  return launch_gemm_mb<BITS, SYM, INTER, 4>(ops, count, M, stream);
+}
+
 template <int BITS, bool SYM, bool INTER>
 hipError_t launch_gemv_t(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
   if (M == 1) {
@@ -1263,10 +1553,17 @@ hipError_t launch_gemv_t(const GemvOperand* ops, int count, int64_t M, hipStream
 
 template <int BITS, bool SYM, bool INTER>
 hipError_t launch_dequantize_t(const DequantProblem& p, hipStream_t stream) {
-  const int64_t total = p.N * (p.K / (32 / BITS));
-  hipLaunchKernelGGL((dequantize_kernel<BITS, SYM, INTER>), dim3(elementwise_blocks(total)), dim3(kElemThreads),
-                     0, stream, p.qweight, p.scales, p.zeros, p.out, total, static_cast<int>(p.K),
-                     static_cast<int>(p.group_size));
+  constexpr int PER = 32 / BITS;
+  const int64_t wpr = p.K / PER;
+  const int64_t wpg = p.group_size / PER;
+  const int gshift = p.group_size == p.K ? 0 : log2_exact(wpg);
+  // x: enough blocks to cover a row's words (up to 4 per CU's worth); y: rows,
+  // walked with a stride beyond 65535
+  const int gx = static_cast<int>(std::min<int64_t>((wpr + kElemThreads - 1) / kElemThreads, 64));
+  const int gy = static_cast<int>(std::min<int64_t>(p.N, 65535));
+  hipLaunchKernelGGL((dequantize_kernel<BITS, SYM, INTER>), dim3(gx, gy), dim3(kElemThreads), 0, stream, p.qweight,
+                     p.scales, p.zeros, p.out, static_cast<int>(p.N), static_cast<int>(p.K),
+                     static_cast<int>(p.group_size), gshift);
   return hipGetLastError();
 }
 
@@ -1323,6 +1620,16 @@ hipError_t launch_gemv_batch(const GemvOperand* ops, int count, int64_t M, int b
   DQ_DISPATCH_12(bits, symmetric, interleaved, DQ_CALL_GEMV)
 #undef DQ_CALL_GEMV
 }
+
+hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
+                             bool interleaved, hipStream_t stream) {
+  if (count < 1 || count > kMaxBatch || M < 1 || M > kMaxGemmM) return hipErrorInvalidValue;
+#define DQ_CALL_GEMM(B, S, I) launch_gemm_t<B, S, I>(ops, count, M, stream)
+  DQ_DISPATCH_12(bits, symmetric, interleaved, DQ_CALL_GEMM)
+#undef DQ_CALL_GEMM
+}
+
+void plan_gemm_batch(const GemvOperand* ops, int count, int bits, int* wk) { gemm_waves_per_tile(ops, count, bits, wk); }
 
 hipError_t launch_dequantize(const DequantProblem& p, hipStream_t stream) {
 #define DQ_CALL_DEQ(B, S, I) launch_dequantize_t<B, S, I>(p, stream)

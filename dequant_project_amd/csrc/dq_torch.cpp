@@ -112,6 +112,27 @@ std::vector<torch::Tensor> gemv_batched(std::vector<torch::Tensor> xs, std::vect
   return ys;
 }
 
+// Fused small GEMM for 1 <= M <= DQ_MAX_GEMM_M (no reference counterpart; see
+// dq_gemm_small): the product the reference's M > 8 path (dequantize, then
+// F.linear over the fp16 weight) computes, in one pass over the packed bytes.
+torch::Tensor gemm_small(torch::Tensor x, torch::Tensor qweight, torch::Tensor scales,
+                         std::optional<torch::Tensor> zeros, int64_t bits, int64_t group_size, bool symmetric,
+                         bool interleaved) {
+  const dq_tensor dx = describe(x), dw = describe(qweight), ds = describe(scales);
+  dq_tensor dz{};
+  if (zeros) dz = describe(*zeros);
+  raise_if(dq_check_gemm_small(&dx, &dw, &ds, zeros ? &dz : nullptr, bits, group_size, symmetric));
+
+  const c10::DeviceGuard guard(x.device());
+  const int64_t M = x.size(0), K = x.size(1), N = qweight.size(0);
+  auto y = torch::empty({M, N}, x.options());
+  const dq_gemv_problem prob{half_ptr(x), reinterpret_cast<const uint32_t*>(qweight.data_ptr()), half_ptr(scales),
+                             zeros ? half_ptr(*zeros) : nullptr, reinterpret_cast<uint16_t*>(y.data_ptr()), N, K,
+                             group_size};
+  raise_if(dq_gemm_small(&prob, 1, M, bits, symmetric, interleaved, current_stream(x)));
+  return y;
+}
+
 // kernels/dequant_gemv.cu:310-337
 torch::Tensor dequantize(torch::Tensor qweight, torch::Tensor scales, std::optional<torch::Tensor> zeros,
                          int64_t bits, int64_t group_size, bool symmetric, bool interleaved, int64_t K) {
@@ -150,6 +171,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemv_batched", &gemv_batched, "grouped packed-weight GEMVs of one format in one launch",
         py::arg("xs"), py::arg("qweights"), py::arg("scales"), py::arg("zeros"), py::arg("bits"),
         py::arg("group_sizes"), py::arg("symmetric"), py::arg("interleaved"));
+  m.def("gemm_small", &gemm_small, "packed-weight GEMM for 1 <= M <= 64: x @ dequantize(W)^T in one pass",
+        py::arg("x"), py::arg("qweight"), py::arg("scales"), py::arg("zeros"), py::arg("bits"),
+        py::arg("group_size"), py::arg("symmetric"), py::arg("interleaved"));
   m.def("dequantize", &dequantize, "materialize a packed weight as fp16 [N,K]", py::arg("qweight"),
         py::arg("scales"), py::arg("zeros"), py::arg("bits"), py::arg("group_size"), py::arg("symmetric"),
         py::arg("interleaved"), py::arg("K"));

@@ -6,8 +6,15 @@ Public surface of the reference's dequant/quant_linear.py (MAX_M :39, PROJ
 
   M <= MAX_M   the fused dequant + GEMV kernel (dequant_cuda.gemv): codes are
                unpacked in registers, nothing is materialized. The decode path.
-  M >  MAX_M   dequant_cuda.dequantize materializes the fp16 [N, K] weight
-               (bit-exact with packer.dequantize) and F.linear does the GEMM.
+  M <= MAX_M_GEMM (no reference counterpart) the fused small GEMM
+               (dequant_cuda.gemm_small): the reference's M > MAX_M product,
+               x @ dequantize(W)^T over the same fp16 weight, formed in
+               registers in one pass over the packed bytes instead of
+               materializing it; equal to the path below up to the order of
+               the fp32 summation.
+  M >  MAX_M_GEMM  dequant_cuda.dequantize materializes the fp16 [N, K] weight
+               (bit-exact with packer.dequantize) and F.linear does the GEMM
+               (the reference's branch for every M > MAX_M).
 
 Both branches launch on the current HIP stream and never synchronize, so a
 forward pass can be captured into a HIP graph (torch.cuda.CUDAGraph). There is
@@ -24,6 +31,10 @@ from .packer import PackedWeight, QuantConfig, quantize_tensor
 
 # Largest batch the fused kernel handles; above it the dequantize fallback runs.
 MAX_M = 8
+
+# Largest batch the fused small GEMM takes (batched decode, short prefills);
+# above it dequantize + F.linear runs. No reference counterpart.
+MAX_M_GEMM = 64
 
 # The projections of a Llama-style decoder layer that quantize_model replaces.
 PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
@@ -69,6 +80,18 @@ def gemv_grouped(xs, pws):
     return [y.view(*x.shape[:-1], pw.shape[0]) for y, x, pw in zip(ys, xs, pws)]
 
 
+def gemm_small(x, pw: PackedWeight):
+    """y = x @ dequantize(W)^T for up to MAX_M_GEMM rows, in one pass over the
+    packed weight (no reference counterpart; see the module docstring)."""
+    n, k = pw.shape
+    cfg = pw.config
+    x2 = x.reshape(-1, k).contiguous()
+    y = _get_ext().gemm_small(x2, pw.qweight, pw.scales, pw.zeros, cfg.bits,
+                              cfg.effective_group_size(k), cfg.symmetric,
+                              cfg.layout == "interleaved")
+    return y.view(*x.shape[:-1], n)
+
+
 def dequantize_cuda(pw: PackedWeight):
     """fp16 [N, K] on the GPU, bit-exact with packer.dequantize."""
     n, k = pw.shape
@@ -110,6 +133,8 @@ class QuantLinear(nn.Module):
         m = x.numel() // self.in_features
         if m <= MAX_M:
             y = gemv(x, pw)
+        elif m <= MAX_M_GEMM:
+            y = gemm_small(x, pw)
         else:
             y = F.linear(x, dequantize_cuda(pw))
         if self.bias is not None:

@@ -105,6 +105,12 @@ typedef struct dq_tensor {
 int dq_check_gemv(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor* scales,
                   const dq_tensor* zeros, int64_t bits, int64_t group_size, int symmetric);
 
+/* Validation of dequant_cuda.gemm_small(x, qweight, scales, zeros, bits,
+ * group_size, symmetric, interleaved): the rules of dq_check_gemv with
+ * 1 <= M <= DQ_MAX_GEMM_M (no reference counterpart; see dq_gemm_small). */
+int dq_check_gemm_small(const dq_tensor* x, const dq_tensor* qweight, const dq_tensor* scales,
+                        const dq_tensor* zeros, int64_t bits, int64_t group_size, int symmetric);
+
 /* Validation of dequant_cuda.dequantize(..., K): kernels/dequant_gemv.cu:310-317
  * with check_weight :230-283. */
 int dq_check_dequantize(const dq_tensor* qweight, const dq_tensor* scales, const dq_tensor* zeros,
@@ -157,6 +163,20 @@ typedef struct dq_gemv_problem {
  * launch its decode path would use to avoid per-launch overhead. */
 int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
                     int interleaved, dq_stream_t stream);
+
+/* Largest batch (rows of x) of dq_gemm_small. */
+#define DQ_MAX_GEMM_M 64
+
+/* Fused small GEMM: y[M, N] = fp16_rn( x[M, K] @ W16^T ), fp32 accumulation,
+ * for 1 <= M <= DQ_MAX_GEMM_M, over up to DQ_MAX_BATCH problems of one format
+ * (operand rules of dq_gemv_batched). W16 is the fp16 weight dq_dequantize
+ * writes (packer.py:177-189), formed in registers and never stored. No
+ * reference counterpart: it replaces, for batches of 9..64 rows, the
+ * reference's dequantize + F.linear pair (dequant/quant_linear.py:131-132)
+ * with one pass over the packed bytes; results equal that pair's up to the
+ * order of the fp32 summation. */
+int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
+                  int interleaved, dq_stream_t stream);
 
 /* Geometry the launch of these problems would use (no reference
  * counterpart), for profiling and tuning tools; pure host logic. For each

@@ -264,6 +264,67 @@ def test_gemv_zero_points_beyond_fp16_exact_range(torch_gpu):
                    deq_ref=False)
 
 
+# ------------------------------------------------- fused small GEMM (M <= 64)
+def check_gemm_small(torch, pw, qw, sc, ze, ms, label):
+    """gemm_small against fp64 x @ W16^T, W16 = the oracle's packer.dequantize
+    (the reference's M > 8 product): the reference's elementwise fp32
+    criterion on that weight and rel-L2 <= 1e-3."""
+    n, k = pw.shape
+    cfg = P.Config(pw.config.bits, pw.config.group_size, pw.config.symmetric, pw.config.layout)
+    w16 = P.dequantize(qw, sc, ze, cfg, (n, k)).astype(np.float64)
+    for m in ms:
+        x16 = activations(m, k, seed=100 + m)
+        y = ext().gemm_small(to_gpu(torch, x16), *ext_args(pw)).cpu().numpy()
+        ref = x16.astype(np.float64) @ w16.T
+        absref = np.abs(x16.astype(np.float64)) @ np.abs(w16).T
+        ok, worst = P.gemv_criterion(y, ref, absref)
+        rl2 = P.rel_l2(y, ref)
+        print(f"{label} M={m}: worst={worst:.3f}x tol rel_l2={rl2:.2e}", flush=True)
+        assert ok, f"{label} M={m}: elementwise criterion violated, worst {worst:.3f}x tol"
+        assert rl2 <= REL_L2_TOL, f"{label} M={m}: rel-L2 {rl2:.3e}"
+
+
+GEMM_SMALL_CASES = [
+    ((4, 128, False, "sequential"), 1000, 4096),
+    ((4, 32, True, "interleaved"), 256, 96),       # 3 chunks: a partial iteration of 4
+    ((2, 64, False, "sequential"), 512, 3072),     # 4 groups per MFMA iteration
+    ((2, 128, True, "interleaved"), 384, 1024),
+    ((8, None, True, "sequential"), 1100, 4096),   # per-channel
+    ((8, 64, False, "interleaved"), 640, 2048),
+]
+
+
+@pytest.mark.parametrize("fmt,n,k", GEMM_SMALL_CASES, ids=[f"{c[0]}-{c[1]}x{c[2]}" for c in GEMM_SMALL_CASES])
+def test_gemm_small_matches_dequantized_product(torch_gpu, fmt, n, k):
+    torch = torch_gpu
+    pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(n, k, seed=n + k), *fmt)
+    check_gemm_small(torch, pw, qw, sc, ze, (1, 9, 16, 17, 33, 64), f"gemm_small {fmt} [{n},{k}]")
+
+
+def test_gemm_small_zero_points_beyond_fp16_exact_range(torch_gpu):
+    """Bands of far-offset rows (zero points past -1024) take W16 from fp32
+    arithmetic; the result must still be the dequantized weight's product."""
+    torch = torch_gpu
+    n, k = 256, 2048
+    for fmt, base in [((4, 128, False, "sequential"), 50.0), ((2, 64, False, "interleaved"), 200.0),
+                      ((8, 128, False, "sequential"), 3.0)]:
+        w = gauss_weight(n, k, seed=41).astype(np.float32)
+        band = (np.arange(n) // 16) % 2 == 1
+        u = np.random.Generator(np.random.PCG64(42)).random((n, k), dtype=np.float32)
+        w[band] = base + 0.5 * u[band]
+        pw, qw, sc, ze = pack_on_gpu(torch, w.astype(np.float16), *fmt)
+        assert (np.abs(ze.astype(np.float32)[band]) > 1024).all()
+        check_gemm_small(torch, pw, qw, sc, ze, (12, 40), f"gemm_small wide zeros {fmt}")
+
+
+def test_gemm_small_rejects_batches_past_its_range(torch_gpu):
+    torch = torch_gpu
+    pw, _, _, _ = pack_on_gpu(torch, gauss_weight(64, 256, seed=5), 4, 128, False, "sequential")
+    x = torch.zeros(65, 256, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="gemm_small handles 1 <= M <= 64, got M=65"):
+        ext().gemm_small(x, *ext_args(pw))
+
+
 # ------------------------------------------------------- benchmark configs
 def test_config_c1_int4_asym_g128(torch_gpu):
     torch = torch_gpu

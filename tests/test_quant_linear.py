@@ -25,7 +25,7 @@ from torch import nn
 
 from dequant_project_amd import packer
 from dequant_project_amd.packer import QuantConfig, quantize_tensor
-from dequant_project_amd.quant_linear import MAX_M, PROJ, QuantLinear, quantize_model
+from dequant_project_amd.quant_linear import MAX_M, MAX_M_GEMM, PROJ, QuantLinear, quantize_model
 from oracle import packer_ref as P
 
 
@@ -153,7 +153,7 @@ def test_gemv_on_3d_input(torch_gpu):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", [(1, 3072), (8, 3072), (9, 3072), (64, 3072), (2, 32, 3072)])
+@pytest.mark.parametrize("shape", [(1, 3072), (8, 3072), (9, 3072), (64, 3072), (2, 32, 3072), (65, 3072)])
 def test_quant_linear_against_f_linear(torch_gpu, shape):
     """B (scripts/test_quant_linear.py:126-156): both paths of forward, with bias.
 
@@ -177,7 +177,8 @@ def test_quant_linear_against_f_linear(torch_gpu, shape):
     xf = x.float().reshape(m, k)
     ref = xf @ w_ref.T + ql.bias.float()
     absref = xf.abs() @ w_ref.abs().T
-    _check(y.reshape(m, n), ref, absref, 2, f"QuantLinear {shape} M={m} via {'gemv' if m <= MAX_M else 'fallback'}")
+    path = "gemv" if m <= MAX_M else ("gemm_small" if m <= MAX_M_GEMM else "fallback")
+    _check(y.reshape(m, n), ref, absref, 2, f"QuantLinear {shape} M={m} via {path}")
 
 
 @pytest.mark.gpu
