@@ -34,6 +34,8 @@ Printed: ONE JSON line on stdout (progress goes to stderr).
               (the stack step runs one kernel instance), against 8 TB/s
   cpu_baseline  the reference's CPU torch path (oracle/cpu_path.py) on one
               layer of the same stack, on this host's cores
+  other_format_stacks / batch_stacks  the same stack step in INT8 and INT2,
+              and the INT4 stack at M = 2, 4, 8 (C4's other batch sizes)
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 100]
 """
@@ -129,7 +131,7 @@ class Engine:
         self.native.check(st)
         fmt = f"{cfg.bits}, {str(cfg.symmetric).lower()}, {str(cfg.layout == 'interleaved').lower()}"
         if kind.value == 1:
-            return f"gemv_mfma_kernel<{fmt}, {rows.value // 16}>", tuple(wk)
+            return f"gemv_quad_kernel<{fmt}, {rows.value // 4}, {1 if m <= 4 else 2}>", tuple(wk)
         if kind.value in (2, 3):
             return f"gemv_m1_kernel<{fmt}, {rows.value}, {'true' if kind.value == 3 else 'false'}>", tuple(wk)
         mt = 2 if m == 2 else (4 if m <= 4 else 8)
@@ -149,13 +151,18 @@ def build_stack(torch, layers, seed=20251201, cfg=None):
             layer[name] = quantize_tensor(w, cfg)
             del w
         stack.append(layer)
+    return cfg, stack, make_xs(torch, layers, 1, gen)
+
+
+def make_xs(torch, layers, m, gen):
+    """Per layer, the fp16 N(0, 1) inputs [m, K] of its four launch roles."""
     xs = []
     for _ in range(layers):
-        xs.append({"qkv": torch.randn(1, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-                   "o": torch.randn(1, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-                   "gate_up": torch.randn(1, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-                   "down": torch.randn(1, INTER, generator=gen, device="cuda", dtype=torch.float16)})
-    return cfg, stack, xs
+        xs.append({"qkv": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+                   "o": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+                   "gate_up": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+                   "down": torch.randn(m, INTER, generator=gen, device="cuda", dtype=torch.float16)})
+    return xs
 
 
 def step_launches(stack, xs, mode):
@@ -421,6 +428,24 @@ def main():
             del ostack, oxs, launches
             torch.cuda.empty_cache()
 
+    # the same INT4 stack at the other batch sizes the benchmark configs name
+    # (C4: M in {1, 2, 4, 8})
+    batch_stacks = {}
+    if not args.no_extra:
+        gen = torch.Generator(device="cuda").manual_seed(20251203)
+        for m in (2, 4, 8):
+            mxs = make_xs(torch, args.layers, m, gen)
+            launches, step_bytes, ms, per = run_mode(torch, eng, stack, mxs, "stack", args.steps, args.warmup)
+            inst = kernel_instances(eng, launches)
+            batch_stacks[f"M={m}"] = {"launches_per_step": len(launches), "bytes_per_step": step_bytes,
+                                      "ms_per_step": ms, "step_ms": summarize(per),
+                                      "gbs": step_bytes / (ms * 1e-3) / 1e9, "us_per_layer": ms * 1e3 / args.layers,
+                                      "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                                      "kernel_instances": {k: len(v) for k, v in inst.items()}}
+            log(f"stack INT4 M={m}: {ms:.3f} ms/step  {batch_stacks[f'M={m}']['gbs']:.1f} GB/s  "
+                f"{batch_stacks[f'M={m}']['us_per_layer']:.2f} us/layer")
+            del mxs, launches
+
     extra = {}
     if not args.no_extra:
         for name, n, k, c, m in [("C1", 4096, 4096, QuantConfig(4, 128, False), 1),
@@ -455,6 +480,7 @@ def main():
         "cpu_baseline": cpu,
         "modes": modes,
         "other_format_stacks": other_stacks,
+        "batch_stacks": batch_stacks,
         "single_configs": extra,
     }
     print(json.dumps(line, default=lambda o: sorted(o) if isinstance(o, set) else str(o)), flush=True)

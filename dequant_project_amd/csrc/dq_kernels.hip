@@ -960,6 +960,247 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_mfma_kernel(const MfmaBatch
   }
 }
 
+// ------------------------------------------------ quad kernel, 2 <= M <= 8
+// v_mfma_f32_4x4x4_16b_f16 computes 16 independent products D_b += A_b B_b
+// (4x4 by 4x4); lane 4b + j supplies row j of A_b and column j of B_b and
+// holds column j of D_b (register i = row i). Lane l = (b = l/4, q = l%4):
+//   B  chunk cs + b (16 bytes, 128/BITS codes) of weight row row0 + 4g + q,
+//      one register set per quad g of the tile, so one load instruction reads
+//      4 rows x 256 contiguous bytes (as a pure read that pattern reaches
+//      81% of peak; the 16 rows x 64 bytes of a 16x16x32 operand reach 70%);
+//   A  the same chunk's activations of batch row 4mg + q (zeros past M);
+//   D  lane (b, j), register i: sum over chunk cs + b of
+//      x[4mg + i] * (q - z)[row0 + 4g + j].
+// A chunk's MFMAs start from zero and acc += scale * D folds it in with its
+// row's group scale in fp32: the reference's factorized arithmetic (exact
+// (q - z) x products, fp32 sums, one scale per group), as in the VALU
+// kernels, for any group size. The 16 blocks hold different chunks; their
+// sum is taken once per tile (DPP row_ror 4 / 8 inside 16-lane rows, then the
+// gfx950 permlane16 / permlane32 swaps across rows).
+//
+// Zero points outside [-1024, 1024] (WIDE, rare, asymmetric only): the tile
+// is recomputed with q alone for those rows and z * sum(x) subtracted in fp32,
+// sum(x) per chunk and batch row from one more MFMA chain against ones.
+template <int BITS, bool SYM, bool INTER, int NT, int MG, bool WIDE>
+__device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos& t, int M, int blk, int q,
+                                          uint32_t magic, f4 (&acc)[NT][MG], bool& wide) {
+  using F = Fmt<BITS>;
+  constexpr int CPL = F::CPL, NF = CPL / 4;
+  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+  const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
+  const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+  const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row);
+  const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row);
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(M) * static_cast<uint32_t>(d.K) * 2u);
+  uint32_t wrow[NT], mrow[NT];
+#pragma unroll
+  for (int g = 0; g < NT; ++g) {
+    const uint32_t n = static_cast<uint32_t>(min(t.row0 + 4 * g + q, d.N - 1));  // past N: re-read, never stored
+    wrow[g] = n * row_bytes;
+    mrow[g] = n * meta_row;
+  }
+  uint32_t xrow[MG];
+  bool xok[MG];
+#pragma unroll
+  for (int mg = 0; mg < MG; ++mg) {
+    xok[mg] = 4 * mg + q < M;
+    xrow[mg] = static_cast<uint32_t>(4 * mg + q) * static_cast<uint32_t>(d.K) * 2u;
+  }
+  h2 pow_scale[F::NCLS];
+#pragma unroll
+  for (int c = 0; c < F::NCLS; ++c)
+    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
+  for (int cs = t.cb; cs < t.ce; cs += 16) {
+    const int c = cs + blk;
+    const bool ok = c < t.ce;
+    const uint32_t gmo = ok ? group_of(d, c) * 2u : 0u;
+    uint32_t zb[NT], sb[NT];
+    u32x4 w[NT];
+#pragma unroll
+    for (int g = 0; g < NT; ++g)
+      zb[g] = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(zbuf, ok ? mrow[g] + gmo : kOutOfRange, 0, 0);
+#pragma unroll
+    for (int g = 0; g < NT; ++g)
+      sb[g] = __builtin_amdgcn_raw_buffer_load_b16(sbuf, ok ? mrow[g] + gmo : kOutOfRange, 0, 0);
+#pragma unroll
+    for (int g = 0; g < NT; ++g)
+      w[g] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, ok ? wrow[g] + static_cast<uint32_t>(c) * 16u : kOutOfRange,
+                                                   0, 2);
+    u32x4 xv[MG][CPL / 8];
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+      for (int k = 0; k < CPL / 8; ++k)
+        xv[mg][k] = __builtin_amdgcn_raw_buffer_load_b128(
+            xbuf, ok && xok[mg] ? xrow[mg] + static_cast<uint32_t>(c) * (CPL * 2u) + 16u * k : kOutOfRange, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // every load of the step is in flight before the math
+    h2 xp[MG][CPL / 2];
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg) {
+      uint32_t xd[CPL / 2];
+#pragma unroll
+      for (int k = 0; k < CPL / 8; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xd[4 * k + e] = xv[mg][k][e];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp[mg] + j * F::PAIRS);
+    }
+    f4 xs[MG];
+    if constexpr (WIDE) {
+      const h2 one = splat(static_cast<_Float16>(1.0f));
+#pragma unroll
+      for (int mg = 0; mg < MG; ++mg) {
+        xs[mg] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          xs[mg] = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xp[mg][2 * f], xp[mg][2 * f + 1]), cat2(one, one), xs[mg],
+                                                      0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < NT; ++g) {
+      _Float16 zh;
+      bool exact = true;
+      if constexpr (SYM) {
+        zh = static_cast<_Float16>(static_cast<float>(F::BIAS));
+      } else if constexpr (!WIDE) {
+        zh = __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb[g]));
+        wide |= (zb[g] & 0x7FFFu) > 0x6400u;
+      } else {
+        exact = (zb[g] & 0x7FFFu) <= 0x6400u;
+        zh = exact ? __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb[g])) : static_cast<_Float16>(0.0f);
+      }
+      const h2 zz = splat(zh);
+      h2 off[F::NCLS];
+#pragma unroll
+      for (int k = 0; k < F::NCLS; k += 2) {
+        const _Float16 b0 = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(k))));
+        const _Float16 b1 =
+            k + 1 < F::NCLS ? static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(k + 1)))) : b0;
+        const h2 both = -(h2{b0, b1} + zz);
+        off[k] = splat(both.x);
+        if (k + 1 < F::NCLS) off[k + 1] = splat(both.y);
+      }
+      h2 dq[CPL / 2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t mp[F::PAIRS];
+        magic_pairs<BITS>(w[g][j], magic, mp);
+#pragma unroll
+        for (int i = 0; i < F::PAIRS; ++i)
+          dq[j * F::PAIRS + i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]);
+      }
+      const float s = f16_to_f32(static_cast<uint16_t>(sb[g]));
+#pragma unroll
+      for (int mg = 0; mg < MG; ++mg) {
+        f4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          D = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xp[mg][2 * f], xp[mg][2 * f + 1]), cat2(dq[2 * f], dq[2 * f + 1]),
+                                                 D, 0, 0, 0);
+        if constexpr (WIDE) {
+          const float zf = exact ? 0.0f : f16_to_f32(static_cast<uint16_t>(zb[g]));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) D[i] = __builtin_fmaf(-zf, xs[mg][i], D[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[g][mg][i] = __builtin_fmaf(s, D[i], acc[g][mg][i]);
+      }
+    }
+  }
+}
+
+// Sum of v over the 16 lanes sharing l % 4, returned in lanes 0..15 (row 0;
+// the other rows get partial sums). The gfx950 permlane swaps exchange rows
+// with a zero operand, so one output of each swap is the moved row and the
+// other zeros: (even rows += odd rows), then (lower half += upper half).
+// The pair a swap returns is copied out element by element into named
+// values: used directly inside __builtin_bit_cast, this clang reads element
+// 0 for both (checked in its LLVM IR).
+__device__ __forceinline__ float swap_sum16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), 0u, false, false);
+  const uint32_t a = r[0], b = r[1];
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float swap_sum32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), 0u, false, false);
+  const uint32_t a = r[0], b = r[1];
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float quad_column_sum(float v) {
+  v += dpp_move<0x124, 0xf>(v);  // row_ror:4
+  v += dpp_move<0x128, 0xf>(v);  // row_ror:8: every lane of a 16-lane row has its row's sum
+  return swap_sum32(swap_sum16(v));
+}
+
+// Persistent blocks walk block-tiles like gemv_kernel; a tile is 4 * NT rows
+// and the wk waves of a tile split its chunks (in steps of 16), meeting in LDS.
+template <int BITS, bool SYM, bool INTER, int NT, int MG>
+__global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBatch b) {
+  constexpr int NV = NT * MG * 4;  // outputs of one column q per tile: (g, mg, i)
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int blk = lane >> 2, q = lane & 3;
+  __shared__ float part[2][kWavesPerBlock][NV][4];
+  const uint32_t magic = magic_vgpr();
+  const int total = b.bt_start[b.count];
+  int phase = 0;
+  int p = 0;
+  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
+    const TilePos t = locate(b, bt, wave, 4 * NT, p);
+    const KernelProblem& d = b.p[t.p];
+    f4 acc[NT][MG];
+#pragma unroll
+    for (int g = 0; g < NT; ++g)
+#pragma unroll
+      for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
+    if (t.active && t.cb < t.ce) {
+      bool wide = false;
+      quad_tile<BITS, SYM, INTER, NT, MG, false>(d, t, b.M, blk, q, magic, acc, wide);
+      if (!SYM && __builtin_amdgcn_ballot_w64(wide) != 0) {
+#pragma unroll
+        for (int g = 0; g < NT; ++g)
+#pragma unroll
+          for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
+        quad_tile<BITS, SYM, INTER, NT, MG, true>(d, t, b.M, blk, q, magic, acc, wide);
+      }
+    }
+    float tot[NV];
+#pragma unroll
+    for (int g = 0; g < NT; ++g)
+#pragma unroll
+      for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tot[(g * MG + mg) * 4 + i] = quad_column_sum(acc[g][mg][i]);
+    // value v = (g, mg, i) is y[4 mg + i][row0 + 4 g + q]; lane (b = v % 4, q) of row 0 stores it
+    if (t.wk == 1) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const int g = v / (MG * 4), m = 4 * ((v / 4) % MG) + (v % 4), n = t.row0 + 4 * g + q;
+        if (blk == (v & 3) && t.active && m < b.M && n < d.N)
+          d.y[static_cast<int64_t>(m) * d.N + n] = f32_to_f16_rn(tot[v]);
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        if (blk == (v & 3)) part[phase][wave][v][q] = tot[v];
+      __syncthreads();  // all 4 waves of the block run the same block-tile sequence
+      if (t.active && t.kw == 0) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          const int g = v / (MG * 4), m = 4 * ((v / 4) % MG) + (v % 4), n = t.row0 + 4 * g + q;
+          if (blk == (v & 3) && m < b.M && n < d.N) {
+            float s = 0.f;
+            for (int j = 0; j < t.wk; ++j) s += part[phase][wave + j][v][q];
+            d.y[static_cast<int64_t>(m) * d.N + n] = f32_to_f16_rn(s);
+          }
+        }
+      }
+      phase ^= 1;
+    }
+  }
+}
+
 // ---------------------------------------------------- small GEMM, M <= 64 (MFMA)
 // y[m, n] = fp16( sum_k x[m, k] * W16[n, k] ) with W16 = fp16((q - z) * s),
 // the fp16 weight packer.dequantize materializes (packer.py:177-189), built
@@ -1353,12 +1594,13 @@ int resident_blocks() {
   return cached;
 }
 
-template <int BITS, bool SYM, bool INTER, int MT, int R>
-hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
-  constexpr int CPL = 128 / BITS;
-  int wks[kMaxBatch];
-  waves_per_tile(ops, count, BITS, R, wks);
-  KernelBatch kb{};
+// The launch description of a list of problems cut into tiles of R rows
+// whose K ranges wk[i] waves share; a wave's share is a multiple of `step`
+// chunks. Returns the number of block-tiles.
+int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, int R, int step, const int* wks,
+                      KernelBatch& kb) {
+  const int cpl = 128 / bits;
+  kb = KernelBatch{};
   kb.count = count;
   kb.M = static_cast<int>(M);
   int bts = 0;
@@ -1373,18 +1615,27 @@ hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream
     k.N = static_cast<int>(o.N);
     k.K = static_cast<int>(o.K);
     k.n_groups = static_cast<int>(o.K / o.group_size);
-    k.chunks_per_group = static_cast<int>(o.group_size / CPL);
+    k.chunks_per_group = static_cast<int>(o.group_size / cpl);
     k.cpg_shift = log2_exact(k.chunks_per_group);
-    k.n_chunks = static_cast<int>(o.K / CPL);
+    k.n_chunks = static_cast<int>(o.K / cpl);
     const int wk = wks[i];
     k.lwk = log2_exact(wk);
-    k.per_wave = (k.n_chunks + wk - 1) / wk;
+    k.per_wave = ((k.n_chunks + wk - 1) / wk + step - 1) / step * step;
     k.tiles = static_cast<int>((o.N + R - 1) / R);
     const int tiles_per_bt = kWavesPerBlock / wk;
     kb.bt_start[i] = bts;
     bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
   }
   kb.bt_start[count] = bts;
+  return bts;
+}
+
+template <int BITS, bool SYM, bool INTER, int MT, int R>
+hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+  int wks[kMaxBatch];
+  waves_per_tile(ops, count, BITS, R, wks);
+  KernelBatch kb;
+  const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
   if (bts == 0) return hipSuccess;
   if constexpr (MT == 1) {
     constexpr bool MF = m1_uses_mfma(BITS);
@@ -1394,6 +1645,23 @@ hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream
     constexpr auto kernel = gemv_kernel<BITS, SYM, INTER, MT, R, kCmax>;
     return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
   }
+}
+
+// Geometry of the quad kernel (2 <= M <= 8): tiles of 4 * kQuadsPerTile rows,
+// MG = 1 batch-row group of 4 for M <= 4, else 2; wk as for the M = 1 kernel
+// (tiles of 16 rows), each wave's share rounded up to whole steps of 16 chunks.
+constexpr int kQuadsPerTile = 4;
+
+template <int BITS, bool SYM, bool INTER, int MG>
+hipError_t launch_gemv_quad(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+  constexpr int R = 4 * kQuadsPerTile;
+  int wks[kMaxBatch];
+  waves_per_tile(ops, count, BITS, R, wks);
+  KernelBatch kb;
+  const int bts = fill_kernel_batch(ops, count, M, BITS, R, 16, wks, kb);
+  if (bts == 0) return hipSuccess;
+  constexpr auto kernel = gemv_quad_kernel<BITS, SYM, INTER, kQuadsPerTile, MG>;
+  return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
 }
 
 // Geometry of the MFMA kernel (2 <= M <= 8):
@@ -1540,15 +1808,8 @@ hipError_t launch_gemv_t(const GemvOperand* ops, int count, int64_t M, hipStream
     if (rows_per_tile(ops, count, M) == 8) return launch_gemv_r<BITS, SYM, INTER, 1, 8>(ops, count, M, stream);
     return launch_gemv_r<BITS, SYM, INTER, 1, 4>(ops, count, M, stream);
   }
-  if (mfma_applies(ops, count, M, BITS)) {
-    const int RB = mfma_row_blocks(ops, count);
-    if (RB == 4) return launch_gemv_mfma<BITS, SYM, INTER, 4>(ops, count, M, stream);
-    if (RB == 2) return launch_gemv_mfma<BITS, SYM, INTER, 2>(ops, count, M, stream);
-    return launch_gemv_mfma<BITS, SYM, INTER, 1>(ops, count, M, stream);
-  }
-  if (M == 2) return launch_gemv_r<BITS, SYM, INTER, 2, 1>(ops, count, M, stream);
-  if (M <= 4) return launch_gemv_r<BITS, SYM, INTER, 4, 1>(ops, count, M, stream);
-  return launch_gemv_r<BITS, SYM, INTER, 8, 1>(ops, count, M, stream);
+  if (M <= 4) return launch_gemv_quad<BITS, SYM, INTER, 1>(ops, count, M, stream);
+  return launch_gemv_quad<BITS, SYM, INTER, 2>(ops, count, M, stream);
 }
 
 template <int BITS, bool SYM, bool INTER>
@@ -1597,10 +1858,10 @@ hipError_t launch_unpack_t(const uint32_t* qweight, int32_t* out, int64_t N, int
   }
 
 void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows, int* mfma) {
-  if (mfma_applies(ops, count, M, bits)) {
+  if (M >= 2) {
     *mfma = 1;
-    *rows = 16 * mfma_row_blocks(ops, count);
-    for (int i = 0; i < count; ++i) wk[i] = mfma_waves_per_tile(ops[i].K, bits);
+    *rows = 4 * kQuadsPerTile;
+    waves_per_tile(ops, count, bits, *rows, wk);
     return;
   }
   *mfma = M == 1 ? (m1_uses_mfma(bits) ? 3 : 2) : 0;

@@ -221,13 +221,14 @@ def test_gemv_plan_geometry():
     assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 2)
     assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 3)  # 172 columns of 64 codes, 43 per wave
     assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 2)  # INT8 wants 8192 waves
-    # 2 <= M <= 8: the MFMA kernel when every group spans whole iterations of
-    # 4 * 128/bits codes; 16-row blocks per tile from the launch size, wk from K.
-    assert plan([(4096, 4096)], m=4) == ([4], 16, 1)
-    assert plan([(14336, 4096)] * 2, m=8) == ([4, 4], 64, 1)
+    # 2 <= M <= 8: gemv_quad_kernel (kind 1) for every format and group size;
+    # 16-row tiles, wk by the M = 1 rule for 16-row tiles.
+    assert plan([(4096, 4096)], m=4) == ([2], 16, 1)
+    assert plan([(14336, 4096)] * 2, m=8) == ([2, 2], 16, 1)
     assert plan([(11008, 4096)], m=4, bits=8, gs=None) == ([4], 16, 1)
-    assert plan([(4096, 11008)], m=4, bits=2, gs=64) == ([1], 1, 0)   # INT2 g64: VALU kernel
-    assert plan([(4096, 4096)], m=2, gs=64) == ([2], 1, 0)             # INT4 g64: VALU kernel
+    assert plan([(4096, 11008)], m=4, bits=2, gs=64) == ([4], 16, 1)
+    assert plan([(4096, 4096)], m=2, gs=64) == ([2], 16, 1)
+    assert plan([(14336, 4096)] * 16, m=2) == ([1] * 16, 16, 1)
     arr = (_native.DqGemvProblem * 1)()
     arr[0].N, arr[0].K, arr[0].group_size = 8, 100, 100
     wk, rows, kind = (ctypes.c_int * 1)(), ctypes.c_int(), ctypes.c_int()

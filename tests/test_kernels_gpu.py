@@ -242,10 +242,11 @@ def test_gemv_skewed_weights_negative_zero_points(torch_gpu):
 
 def test_gemv_zero_points_beyond_fp16_exact_range(torch_gpu):
     """Zero points outside [-1024, 1024] (unclamped, packer.py:136-137): (q - z)
-    is then not exact in fp16 and the M = 1 kernel takes its separate path
-    (q exactly, minus z * sum(x) in fp32) for the batches that hold one.
-    Bands of 8 rows of far-offset weights alternate with N(0, 0.02) rows, so
-    tiles mix both kinds; every M = 1 kernel variant (VALU and MFMA dots) is
+    is then not exact in fp16 and the kernels take their separate path (q
+    exactly, minus z * sum(x) in fp32) for the tiles that hold one. Bands of 8
+    rows of far-offset weights alternate with N(0, 0.02) rows, so tiles mix
+    both kinds; every M = 1 kernel variant (VALU and MFMA dots) and both
+    batch-row groupings of the 2 <= M <= 8 kernel (M <= 4, M > 4) are
     covered."""
     torch = torch_gpu
     n, k = 256, 4096
@@ -260,7 +261,7 @@ def test_gemv_zero_points_beyond_fp16_exact_range(torch_gpu):
         pw, qw, sc, ze = pack_on_gpu(torch, w.astype(np.float16), *fmt)
         zf = ze.astype(np.float32)
         assert (np.abs(zf[band]) > 1024).all() and (np.abs(zf[~band]) <= 1024).all(), fmt
-        check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=33) for m in (1, 8)], f"wide zeros {fmt}",
+        check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=33) for m in (1, 3, 8)], f"wide zeros {fmt}",
                    deq_ref=False)
 
 
