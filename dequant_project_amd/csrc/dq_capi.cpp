@@ -20,6 +20,8 @@
 #include "dq_internal.h"
 
 static_assert(DQ_MAX_BATCH == dq::kMaxBatch, "batch limits of the ABI and the kernels differ");
+static_assert(DQ_PROLOGUE_RMSNORM == dq::kPrologueRmsNorm && DQ_PROLOGUE_SWIGLU == dq::kPrologueSwiGlu,
+              "prologue codes of the ABI and the kernels differ");
 
 namespace {
 
@@ -325,6 +327,41 @@ int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64
   if (live == 0) return DQ_OK;
   return launch_status(dq::launch_gemv_batch(ops, live, M, static_cast<int>(bits), symmetric != 0,
                                              interleaved != 0, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dq_gemv_prologue_batched(const dq_gemv_problem* problems, const void* const* aux, int count, int64_t M,
+                             int64_t bits, int symmetric, int interleaved, int prologue, float eps,
+                             dq_stream_t stream) {
+  g_error.clear();
+  if (count < 1 || count > DQ_MAX_BATCH)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("count must be in [1, ", DQ_MAX_BATCH, "], got ", count));
+  if (!problems || !aux) return fail(DQ_ERR_INVALID_ARGUMENT, "problems and aux must not be NULL");
+  if (prologue != DQ_PROLOGUE_RMSNORM && prologue != DQ_PROLOGUE_SWIGLU)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("unknown prologue ", prologue));
+  if (prologue == DQ_PROLOGUE_RMSNORM && !(eps >= 0.0f && eps < 1e30f))
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("eps must be finite and non-negative, got ", eps));
+  if (M != 1) return fail(DQ_ERR_UNSUPPORTED, cat("fused prologues handle M = 1, got M=", M));
+  dq::GemvOperand ops[DQ_MAX_BATCH];
+  int live = 0;
+  for (int i = 0; i < count; ++i) {
+    const dq_gemv_problem& p = problems[i];
+    int st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, M, p.N, p.K, bits, p.group_size,
+                                symmetric);
+    if (!st && !aux[i]) st = fail(DQ_ERR_INVALID_ARGUMENT, "aux must not be NULL");
+    if (!st && !aligned16(aux[i])) st = fail(DQ_ERR_INVALID_ARGUMENT, "aux must be 16-byte aligned");
+    if (st) {
+      g_error = cat("problem ", i, ": ", g_error);
+      return st;
+    }
+    if (p.N > 0) {
+      ops[live] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
+      ops[live++].aux = static_cast<const uint16_t*>(aux[i]);
+    }
+  }
+  if (live == 0) return DQ_OK;
+  return launch_status(dq::launch_gemv_prologue_batch(ops, live, M, static_cast<int>(bits), symmetric != 0,
+                                                      interleaved != 0, prologue, eps,
+                                                      reinterpret_cast<hipStream_t>(stream)));
 }
 
 int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,

@@ -20,6 +20,7 @@ struct GemvOperand {
   const uint16_t* zeros;    // fp16 [N, K/group_size] or nullptr (symmetric)
   uint16_t* y;              // fp16 [M, N]
   int64_t N, K, group_size;
+  const uint16_t* aux = nullptr;  // prologue operand: RMSNorm gamma fp16 [K] or SwiGLU up fp16 [M, K]
 };
 
 // Profiling hook: when both events are non-null, the next GEMV launch on this
@@ -38,6 +39,16 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
 // All problems of one launch share M and the format (bits, symmetry, layout).
 hipError_t launch_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
                              bool interleaved, hipStream_t stream);
+
+// Activation prologues of launch_gemv_prologue_batch (every problem's `aux`
+// must be set): y = W (rmsnorm(x) * gamma) with aux = gamma [K] and eps, or
+// y = W (silu(x) * up) with aux = up [M, K] (x = the gate projection's output).
+constexpr int kPrologueRmsNorm = 1;
+constexpr int kPrologueSwiGlu = 2;
+
+// launch_gemv_batch with an activation prologue; M = 1.
+hipError_t launch_gemv_prologue_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
+                                      bool interleaved, int prologue, float eps, hipStream_t stream);
 
 // Largest M the small fused GEMM takes (launch_gemm_batch).
 constexpr int kMaxGemmM = 64;

@@ -220,6 +220,7 @@ struct KernelProblem {
   const uint16_t* zeros;
   const uint16_t* x;
   uint16_t* y;
+  const uint16_t* aux;   // prologue operand (gamma [K] or up [M, K]); unused without one
   int N, K;
   int n_groups;          // K / group_size
   int chunks_per_group;  // group_size / (128/BITS)
@@ -235,6 +236,7 @@ struct KernelBatch {
   int bt_start[kMaxBatch + 1];  // prefix sums of block-tiles (4/wk tiles each); blocks never mix problems
   int count;
   int M;
+  float eps;  // RMSNorm prologue epsilon
 };
 
 // Where block-tile `bt` of the launch sits, as seen by one wave. All fields
@@ -365,6 +367,82 @@ __device__ __forceinline__ void load_x_columns(const KernelProblem& d, const Til
 #pragma unroll
     for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xr[ct][j]);
   }
+}
+
+// Activation prologues fused into the GEMV (one choice per launch):
+//   kProNone     x as given;
+//   kProRmsNorm  RMSNorm folded in: the activation pairs are x * gamma (fp16
+//                products; gamma = aux, [K]) and ssq accumulates sum(x^2) in
+//                fp32 over the wave's chunks; each row's dot product is
+//                multiplied by 1/sqrt(sum(x^2)/K + eps) when its tile finishes
+//                (the factor is common to the whole row of the product);
+//   kProSwiGlu   SwiGLU folded in: x is the gate projection's output and aux
+//                the up projection's ([M, K]); the pairs are
+//                fp16(fp16(silu(gate)) * up) with silu(g) = g / (1 + e^-g) in
+//                fp32, the roundings of the unfused fp16 ops.
+enum : int { kProNone = 0, kProRmsNorm = kPrologueRmsNorm, kProSwiGlu = kPrologueSwiGlu };
+
+__device__ __forceinline__ _Float16 silu_h(_Float16 g) {
+  const float gf = static_cast<float>(g);
+  const float e = __builtin_amdgcn_exp2f(-gf * 1.4426950408889634f);  // e^-g
+  return static_cast<_Float16>(gf * __builtin_amdgcn_rcpf(1.0f + e));
+}
+
+__device__ __forceinline__ uint32_t swiglu_pair(uint32_t g, uint32_t u) {
+  const h2 gh = as_h2(g);
+  const h2 sh = h2{silu_h(gh.x), silu_h(gh.y)};
+  return __builtin_bit_cast(uint32_t, sh * as_h2(u));  // fp16 product: the exact product rounded once
+}
+
+// Raw activation (and prologue operand) dwords of one chunk column per lane
+// for batch row m: loads only, so they can be issued ahead of the tile's.
+template <int BITS, int PRO>
+struct XRaw {
+  uint32_t x[Fmt<BITS>::CPL / 2];
+  uint32_t a[PRO == kProNone ? 1 : Fmt<BITS>::CPL / 2];
+};
+
+template <int BITS, int PRO>
+__device__ __forceinline__ void issue_x_pro(const KernelProblem& d, const TilePos& t, int lane, int m, int M,
+                                            XRaw<BITS, PRO>& R) {
+  using F = Fmt<BITS>;
+  const uint32_t kb = static_cast<uint32_t>(d.K) * 2u;
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(M) * kb);
+  const __amdgpu_buffer_rsrc_t abuf = buffer_of(d.aux, (PRO == kProSwiGlu ? static_cast<uint32_t>(M) : 1u) * kb);
+  const uint32_t xoff = column_offset(t.cb + lane, t.ce, F::CPL * 2u);
+  const uint32_t mrow = static_cast<uint32_t>(m) * kb;
+#pragma unroll
+  for (int q = 0; q < F::CPL / 8; ++q) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xbuf, xoff + 16u * q, mrow, 0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) R.x[4 * q + e] = v[e];
+  }
+  if constexpr (PRO != kProNone) {
+#pragma unroll
+    for (int q = 0; q < F::CPL / 8; ++q) {
+      const u32x4 v =
+          __builtin_amdgcn_raw_buffer_load_b128(abuf, xoff + 16u * q, PRO == kProSwiGlu ? mrow : 0u, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) R.a[4 * q + e] = v[e];
+    }
+  }
+}
+
+// The prologue's arithmetic on loaded dwords, then the pair order of the math.
+template <int BITS, bool INTER, int PRO>
+__device__ __forceinline__ void x_pairs_pro(XRaw<BITS, PRO>& R, h2 (&xr)[4][Fmt<BITS>::PAIRS], float& ssq) {
+  using F = Fmt<BITS>;
+#pragma unroll
+  for (int i = 0; i < F::CPL / 2; ++i) {
+    if constexpr (PRO == kProRmsNorm) {
+      ssq = __builtin_amdgcn_fdot2(as_h2(R.x[i]), as_h2(R.x[i]), ssq, false);
+      R.x[i] = __builtin_bit_cast(uint32_t, as_h2(R.x[i]) * as_h2(R.a[i]));
+    } else if constexpr (PRO == kProSwiGlu) {
+      R.x[i] = swiglu_pair(R.x[i], R.a[i]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(R.x + j * (F::PER / 2), xr[j]);
 }
 
 // The math of one tile for one batch row m: yacc[r] gets sum over the wave's
@@ -548,12 +626,19 @@ __device__ __forceinline__ void tile_math_m1(const TileLoads<BITS, R, 1>& L, con
 // loaded registers: it re-reads the activations, and each row's weights,
 // scale and zero in a rolled loop, so it adds little to the kernel's register
 // budget; results rotate into acc[] in row order.
-template <int BITS, bool INTER, int R, bool MF>
+template <int BITS, bool INTER, int R, bool MF, int PRO>
 __device__ __forceinline__ void tile_math_m1_wide_zeros(const KernelProblem& d, const TilePos& tb, int lane,
                                                         uint32_t magic, float (&acc)[R]) {
   using F = Fmt<BITS>;
   h2 xr[1][4][F::PAIRS];
-  load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
+  if constexpr (PRO == kProNone) {
+    load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
+  } else {
+    XRaw<BITS, PRO> raw;
+    issue_x_pro<BITS, PRO>(d, tb, lane, 0, 1, raw);
+    float unused = 0.f;
+    x_pairs_pro<BITS, INTER, PRO>(raw, xr[0], unused);
+  }
   float xsum = 0.f;
   const h2 one = splat(static_cast<_Float16>(1.0f));
 #pragma unroll
@@ -589,13 +674,51 @@ __device__ __forceinline__ void tile_math_m1_wide_zeros(const KernelProblem& d, 
   for (int r = 0; r < R; ++r) acc[r] = res[r];
 }
 
-template <int BITS, bool SYM, bool INTER, int R, bool MF>
+// finish_tile for the RMSNorm prologue: the R dot products and the wave's
+// sum(x^2) are reduced together (and combined over the wk waves of a split
+// K), then y = dot / sqrt(sum(x^2) / K + eps).
+__device__ __forceinline__ float inv_rms(float ssq, int K, float eps) {
+  return 1.0f / __builtin_sqrtf(ssq / static_cast<float>(K) + eps);
+}
+
+template <int R>
+__device__ __forceinline__ void finish_tile_rms(const KernelProblem& d, const TilePos& t, int wave, int lane, float eps,
+                                                float (&yacc)[R][1], float ssq, float (*part)[R + 1]) {
+  float v[R + 1];
+#pragma unroll
+  for (int r = 0; r < R; ++r) v[r] = yacc[r][0];
+  v[R] = ssq;
+  wave_sum_lane63<R + 1>(v);
+  if (t.wk == 1) {
+    const float f = inv_rms(v[R], d.K, eps);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (t.active && lane == 63 && t.row0 + r < d.N) d.y[t.row0 + r] = f32_to_f16_rn(v[r] * f);
+  } else {
+    if (lane == 63) {
+#pragma unroll
+      for (int i = 0; i <= R; ++i) part[wave][i] = v[i];
+    }
+    __syncthreads();  // all 4 waves of the block run the same block-tile sequence
+    if (t.active && t.kw == 0 && lane < R) {
+      float a = 0.f, q = 0.f;
+      for (int j = 0; j < t.wk; ++j) {
+        a += part[wave + j][lane];
+        q += part[wave + j][R];
+      }
+      if (t.row0 + lane < d.N) d.y[t.row0 + lane] = f32_to_f16_rn(a * inv_rms(q, d.K, eps));
+    }
+  }
+}
+
+template <int BITS, bool SYM, bool INTER, int R, bool MF, int PRO>
 __global__ void __launch_bounds__(kGemvThreads)
 gemv_m1_kernel(const KernelBatch b) {
   using F = Fmt<BITS>;
+  constexpr int PW = PRO == kProRmsNorm ? R + 1 : R;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
-  __shared__ float part[2][kWavesPerBlock][R];
+  __shared__ float part[2][kWavesPerBlock][PW];
   const uint32_t magic = magic_vgpr();
   const int total = b.bt_start[b.count];
   int phase = 0;
@@ -606,6 +729,7 @@ gemv_m1_kernel(const KernelBatch b) {
     float yacc[R][1];
 #pragma unroll
     for (int r = 0; r < R; ++r) yacc[r][0] = 0.f;
+    float ssq = 0.f;  // RMSNorm prologue: this wave's sum(x^2)
     if (t.active) {
       // the batch loop is branch-free; a batch with a zero point outside
       // [-1024, 1024] only sets `wide`, and the tile is then redone below
@@ -618,13 +742,18 @@ gemv_m1_kernel(const KernelBatch b) {
         // math needs them, so with them last no row could start before the
         // whole tile had arrived
         h2 xr[1][4][F::PAIRS];
-        load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
+        XRaw<BITS, PRO> raw;
+        if constexpr (PRO == kProNone)
+          load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
+        else
+          issue_x_pro<BITS, PRO>(d, tb, lane, 0, 1, raw);
         TileLoads<BITS, R, 1> L;
         issue_tile_m1<BITS, SYM, R>(d, tb, lane, L);
         // keep every load of the batch ahead of its math: left alone, the
         // scheduler sinks the weight loads into the math to save registers,
         // leaving one or two rows in flight and the latency exposed per row
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PRO != kProNone) x_pairs_pro<BITS, INTER, PRO>(raw, xr[0], ssq);
         if constexpr (!SYM) {
 #pragma unroll
           for (int r = 0; r < R; ++r) wide |= (L.z[0][r] & 0x7FFFu) > 0x6400u;
@@ -645,13 +774,16 @@ gemv_m1_kernel(const KernelBatch b) {
           tb.cb = cbase;
           tb.ce = min(t.ce, cbase + 64);
           float acc[R];
-          tile_math_m1_wide_zeros<BITS, INTER, R, MF>(d, tb, lane, magic, acc);
+          tile_math_m1_wide_zeros<BITS, INTER, R, MF, PRO>(d, tb, lane, magic, acc);
 #pragma unroll
           for (int r = 0; r < R; ++r) yacc[r][0] += acc[r];
         }
       }
     }
-    finish_tile<R, 1>(d, t, wave, lane, b.M, yacc, part[phase]);
+    if constexpr (PRO == kProRmsNorm)
+      finish_tile_rms<R>(d, t, wave, lane, b.eps, yacc, ssq, part[phase]);
+    else
+      finish_tile<R, 1>(d, t, wave, lane, b.M, yacc, part[phase]);
     if (t.wk > 1) phase ^= 1;
   }
 }
@@ -1612,6 +1744,7 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
     k.zeros = o.zeros;
     k.x = o.x;
     k.y = o.y;
+    k.aux = o.aux;
     k.N = static_cast<int>(o.N);
     k.K = static_cast<int>(o.K);
     k.n_groups = static_cast<int>(o.K / o.group_size);
@@ -1630,16 +1763,17 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
   return bts;
 }
 
-template <int BITS, bool SYM, bool INTER, int MT, int R>
-hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+template <int BITS, bool SYM, bool INTER, int MT, int R, int PRO = kProNone>
+hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
   int wks[kMaxBatch];
   waves_per_tile(ops, count, BITS, R, wks);
   KernelBatch kb;
   const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
+  kb.eps = eps;
   if (bts == 0) return hipSuccess;
   if constexpr (MT == 1) {
     constexpr bool MF = m1_uses_mfma(BITS);
-    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, MF>;
+    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, MF, PRO>;
     return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
   } else {
     constexpr auto kernel = gemv_kernel<BITS, SYM, INTER, MT, R, kCmax>;
@@ -1813,6 +1947,20 @@ hipError_t launch_gemv_t(const GemvOperand* ops, int count, int64_t M, hipStream
 }
 
 template <int BITS, bool SYM, bool INTER>
+hipError_t launch_gemv_prologue_t(const GemvOperand* ops, int count, int64_t M, int prologue, float eps,
+                                  hipStream_t stream) {
+  if (M != 1) return hipErrorInvalidValue;
+  const bool wide_tiles = rows_per_tile(ops, count, M) == 8;
+  if (prologue == kPrologueRmsNorm)
+    return wide_tiles ? launch_gemv_r<BITS, SYM, INTER, 1, 8, kProRmsNorm>(ops, count, M, stream, eps)
+                      : launch_gemv_r<BITS, SYM, INTER, 1, 4, kProRmsNorm>(ops, count, M, stream, eps);
+  if (prologue == kPrologueSwiGlu)
+    return wide_tiles ? launch_gemv_r<BITS, SYM, INTER, 1, 8, kProSwiGlu>(ops, count, M, stream)
+                      : launch_gemv_r<BITS, SYM, INTER, 1, 4, kProSwiGlu>(ops, count, M, stream);
+  return hipErrorInvalidValue;
+}
+
+template <int BITS, bool SYM, bool INTER>
 hipError_t launch_dequantize_t(const DequantProblem& p, hipStream_t stream) {
   constexpr int PER = 32 / BITS;
   const int64_t wpr = p.K / PER;
@@ -1880,6 +2028,14 @@ hipError_t launch_gemv_batch(const GemvOperand* ops, int count, int64_t M, int b
 #define DQ_CALL_GEMV(B, S, I) launch_gemv_t<B, S, I>(ops, count, M, stream)
   DQ_DISPATCH_12(bits, symmetric, interleaved, DQ_CALL_GEMV)
 #undef DQ_CALL_GEMV
+}
+
+hipError_t launch_gemv_prologue_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
+                                      bool interleaved, int prologue, float eps, hipStream_t stream) {
+  if (count < 1 || count > kMaxBatch) return hipErrorInvalidValue;
+#define DQ_CALL_PRO(B, S, I) launch_gemv_prologue_t<B, S, I>(ops, count, M, prologue, eps, stream)
+  DQ_DISPATCH_12(bits, symmetric, interleaved, DQ_CALL_PRO)
+#undef DQ_CALL_PRO
 }
 
 hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,

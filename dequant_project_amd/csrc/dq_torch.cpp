@@ -112,6 +112,52 @@ std::vector<torch::Tensor> gemv_batched(std::vector<torch::Tensor> xs, std::vect
   return ys;
 }
 
+// Grouped GEMV with a fused activation prologue (no reference counterpart; see
+// dq_gemv_prologue_batched): prologue 1 = RMSNorm (auxs[i] = gamma, fp16 [K]),
+// 2 = SwiGLU (xs[i] = gate output, auxs[i] = up output, both fp16 [M, K]).
+std::vector<torch::Tensor> gemv_prologue(std::vector<torch::Tensor> xs, std::vector<torch::Tensor> auxs,
+                                         int64_t prologue, double eps, std::vector<torch::Tensor> qweights,
+                                         std::vector<torch::Tensor> scales,
+                                         std::vector<std::optional<torch::Tensor>> zeros, int64_t bits,
+                                         std::vector<int64_t> group_sizes, bool symmetric, bool interleaved) {
+  const size_t n = xs.size();
+  if (n == 0 || n > DQ_MAX_BATCH)
+    throw std::runtime_error("gemv_prologue takes 1.." + std::to_string(DQ_MAX_BATCH) + " problems");
+  if (auxs.size() != n || qweights.size() != n || scales.size() != n || zeros.size() != n ||
+      group_sizes.size() != n)
+    throw std::runtime_error("gemv_prologue: xs, auxs, qweights, scales, zeros and group_sizes differ in length");
+  std::vector<dq_gemv_problem> probs(n);
+  std::vector<const void*> aux_ptrs(n);
+  std::vector<torch::Tensor> ys;
+  ys.reserve(n);
+  for (size_t i = 0; i < n; ++i) {
+    const dq_tensor dx = describe(xs[i]), dw = describe(qweights[i]), ds = describe(scales[i]);
+    dq_tensor dz{};
+    if (zeros[i]) dz = describe(*zeros[i]);
+    if (dq_check_gemv(&dx, &dw, &ds, zeros[i] ? &dz : nullptr, bits, group_sizes[i], symmetric) != DQ_OK)
+      throw std::runtime_error("problem " + std::to_string(i) + ": " + dq_last_error());
+    if (xs[i].size(0) != xs[0].size(0)) throw std::runtime_error("gemv_prologue: all problems must share M");
+    if (xs[i].device() != xs[0].device()) throw std::runtime_error("gemv_prologue: all problems must share a device");
+    const torch::Tensor& a = auxs[i];
+    const bool shape_ok = prologue == DQ_PROLOGUE_SWIGLU ? a.sizes() == xs[i].sizes()
+                                                         : (a.dim() == 1 && a.size(0) == xs[i].size(1));
+    if (a.scalar_type() != at::kHalf || !a.is_contiguous() || a.device() != xs[i].device() || !shape_ok)
+      throw std::runtime_error("problem " + std::to_string(i) + ": aux must be a contiguous float16 tensor on " +
+                               "x's device, " + (prologue == DQ_PROLOGUE_SWIGLU ? "shaped like x" : "of shape [K]"));
+    aux_ptrs[i] = a.data_ptr();
+    ys.push_back(torch::empty({xs[i].size(0), qweights[i].size(0)}, xs[i].options()));
+    probs[i] = dq_gemv_problem{half_ptr(xs[i]), reinterpret_cast<const uint32_t*>(qweights[i].data_ptr()),
+                               half_ptr(scales[i]), zeros[i] ? half_ptr(*zeros[i]) : nullptr,
+                               reinterpret_cast<uint16_t*>(ys[i].data_ptr()), qweights[i].size(0),
+                               xs[i].size(1), group_sizes[i]};
+  }
+  const c10::DeviceGuard guard(xs[0].device());
+  raise_if(dq_gemv_prologue_batched(probs.data(), aux_ptrs.data(), static_cast<int>(n), xs[0].size(0), bits,
+                                    symmetric, interleaved, static_cast<int>(prologue), static_cast<float>(eps),
+                                    current_stream(xs[0])));
+  return ys;
+}
+
 // Fused small GEMM for 1 <= M <= DQ_MAX_GEMM_M (no reference counterpart; see
 // dq_gemm_small): the product the reference's M > 8 path (dequantize, then
 // F.linear over the fp16 weight) computes, in one pass over the packed bytes.
@@ -171,6 +217,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gemv_batched", &gemv_batched, "grouped packed-weight GEMVs of one format in one launch",
         py::arg("xs"), py::arg("qweights"), py::arg("scales"), py::arg("zeros"), py::arg("bits"),
         py::arg("group_sizes"), py::arg("symmetric"), py::arg("interleaved"));
+  m.def("gemv_prologue", &gemv_prologue,
+        "grouped packed-weight GEMVs (M = 1) with a fused RMSNorm (1) or SwiGLU (2) activation prologue",
+        py::arg("xs"), py::arg("auxs"), py::arg("prologue"), py::arg("eps"), py::arg("qweights"), py::arg("scales"),
+        py::arg("zeros"), py::arg("bits"), py::arg("group_sizes"), py::arg("symmetric"), py::arg("interleaved"));
   m.def("gemm_small", &gemm_small, "packed-weight GEMM for 1 <= M <= 64: x @ dequantize(W)^T in one pass",
         py::arg("x"), py::arg("qweight"), py::arg("scales"), py::arg("zeros"), py::arg("bits"),
         py::arg("group_size"), py::arg("symmetric"), py::arg("interleaved"));

@@ -177,6 +177,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--iters", type=int, default=30)
     ap.add_argument("--fp16-baseline", action="store_true", help="also time the unquantized fp16 model")
+    ap.add_argument("--fused", action="store_true",
+                    help="also time the quantized model with fused RMSNorm / SwiGLU prologues (fused.fuse_llama)")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("decode.py needs a GPU", file=sys.stderr)
@@ -199,17 +201,27 @@ def main(argv=None):
     stats = quantize_model(model, cfg)
     rec["quant"] = {"config": repr(cfg), **stats}
     for n in seq_lens:
-        b = quantized_bytes_per_token(model, n)
-        for mode in modes:
-            t, _ = time_decode(model, n, mode, args.warmup, args.iters)
-            row = {"weights": repr(cfg), "seq_len": n, "mode": mode, **t, "bytes_per_token": b,
-                   "gbs": b / (t["gpu_ms"]["median"] * 1e-3) / 1e9,
-                   "us_per_token": t["gpu_ms" if mode == "graph" else "total_ms"]["median"] * 1e3}
-            rec["rows"].append(row)
-            print(f"{cfg.bits}-bit seq {n} {mode}: {row['us_per_token']:.0f} us/token "
-                  f"(gpu {t['gpu_ms']['median']:.3f} ms, {row['gbs']:.0f} GB/s)", file=sys.stderr)
+        _time_rows(rec, model, cfg, n, modes, args, "unfused")
+    if args.fused:
+        from .fused import fuse_llama
+
+        rec["fused"] = fuse_llama(model)  # in place, after the unfused rows
+        for n in seq_lens:
+            _time_rows(rec, model, cfg, n, modes, args, "fused")
     print(json.dumps(rec))
     return 0
+
+
+def _time_rows(rec, model, cfg, n, modes, args, label):
+    b = quantized_bytes_per_token(model, n)
+    for mode in modes:
+        t, _ = time_decode(model, n, mode, args.warmup, args.iters)
+        row = {"weights": repr(cfg), "prologues": label, "seq_len": n, "mode": mode, **t, "bytes_per_token": b,
+               "gbs": b / (t["gpu_ms"]["median"] * 1e-3) / 1e9,
+               "us_per_token": t["gpu_ms" if mode == "graph" else "total_ms"]["median"] * 1e3}
+        rec["rows"].append(row)
+        print(f"{cfg.bits}-bit {label} seq {n} {mode}: {row['us_per_token']:.0f} us/token "
+              f"(gpu {t['gpu_ms']['median']:.3f} ms, {row['gbs']:.0f} GB/s)", file=sys.stderr)
 
 
 if __name__ == "__main__":

@@ -164,6 +164,28 @@ typedef struct dq_gemv_problem {
 int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
                     int interleaved, dq_stream_t stream);
 
+/* Activation prologues of dq_gemv_prologue_batched. */
+#define DQ_PROLOGUE_RMSNORM 1 /* y = W (rmsnorm(x; eps) * gamma): aux[i] = gamma, fp16 [K] */
+#define DQ_PROLOGUE_SWIGLU 2  /* y = W (silu(x) * up): x = gate output, aux[i] = up, fp16 [M, K] */
+
+/* Grouped GEMV (operand rules of dq_gemv_batched, M = 1) whose activations
+ * first pass through a fused prologue, so the op before a Llama projection
+ * costs no kernel of its own:
+ *   DQ_PROLOGUE_RMSNORM  the RMSNorm in front of q|k|v and gate|up:
+ *     y = W h, h = x / sqrt(mean(x^2) + eps) * gamma (mean over K, in fp32);
+ *     computed as (W (x * gamma)) / sqrt(mean(x^2) + eps), with fp16
+ *     products x * gamma;
+ *   DQ_PROLOGUE_SWIGLU   the SwiGLU in front of down_proj:
+ *     y = W h, h = fp16(fp16(silu(x)) * up), silu(g) = g / (1 + e^-g) in fp32.
+ * aux[i] belongs to problem i (16-byte aligned). No reference counterpart: the
+ * fusion of RMSNorm and SwiGLU into the projections is the reference's planned
+ * next step (MODEL_SELECTION.md:211-218; byte_model.py:227-228 counts those
+ * activation bytes); results match the unfused ops (torch RMSNorm / SiLU * up,
+ * then dq_gemv_batched) to fp16 rounding of the activations. */
+int dq_gemv_prologue_batched(const dq_gemv_problem* problems, const void* const* aux, int count, int64_t M,
+                             int64_t bits, int symmetric, int interleaved, int prologue, float eps,
+                             dq_stream_t stream);
+
 /* Largest batch (rows of x) of dq_gemm_small. */
 #define DQ_MAX_GEMM_M 64
 
@@ -182,13 +204,9 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
  * counterpart), for profiling and tuning tools; pure host logic. For each
  * problem i, waves_per_tile[i] waves (1, 2 or 4) share one tile along K;
  * the launch uses *rows_per_tile output rows per tile and the kernel
- *   *kernel_kind == 0: gemv_kernel<bits, symmetric, interleaved, MT,
- *                      rows_per_tile, 1> (VALU dot products; 2 <= M <= 8,
- *                      MT = 2, 4 or 8, the smallest >= M, when
- *                      gemv_mfma_kernel does not apply),
- *   *kernel_kind == 1: gemv_mfma_kernel<bits, symmetric, interleaved,
- *                      rows_per_tile / 16> (matrix cores; 2 <= M <= 8 when
- *                      every group_size is a multiple of 4 * 128/bits),
+ *   *kernel_kind == 1: gemv_quad_kernel<bits, symmetric, interleaved,
+ *                      rows_per_tile / 4, MG> (matrix cores; 2 <= M <= 8,
+ *                      any group size; MG = 1 for M <= 4, else 2),
  *   *kernel_kind == 2: gemv_m1_kernel<bits, symmetric, interleaved,
  *                      rows_per_tile, false> (M = 1; VALU dot products), or
  *   *kernel_kind == 3: gemv_m1_kernel<bits, symmetric, interleaved,

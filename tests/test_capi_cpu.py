@@ -254,3 +254,35 @@ def test_gemv_batched_validation():
     assert lib.dq_last_error() == b"problem 1: K=250 is not divisible by group_size=128"
     assert lib.dq_set_launch_events(ctypes.c_void_p(0x10), None) == 1
     assert lib.dq_set_launch_events(None, None) == 0
+
+
+def test_gemv_prologue_validation():
+    """dq_gemv_prologue_batched rejects bad arguments before any launch."""
+    lib = _native.capi()
+    arr = (_native.DqGemvProblem * 2)()
+    aux = (ctypes.c_void_p * 2)(0x2000, 0x2000)
+    for i in range(2):
+        arr[i].x = arr[i].qweight = arr[i].scales = arr[i].zeros = arr[i].y = 0x1000
+        arr[i].N, arr[i].K, arr[i].group_size = 4, 256, 128
+    call = lib.dq_gemv_prologue_batched
+    assert call(arr, aux, 0, 1, 4, 0, 0, 1, 1e-5, None) == 1
+    assert lib.dq_last_error() == b"count must be in [1, 16], got 0"
+    assert call(arr, None, 2, 1, 4, 0, 0, 1, 1e-5, None) == 1
+    assert lib.dq_last_error() == b"problems and aux must not be NULL"
+    assert call(arr, aux, 2, 1, 4, 0, 0, 3, 1e-5, None) == 1
+    assert lib.dq_last_error() == b"unknown prologue 3"
+    assert call(arr, aux, 2, 1, 4, 0, 0, 1, -1.0, None) == 1
+    assert b"eps must be finite and non-negative" in lib.dq_last_error()
+    assert call(arr, aux, 2, 1, 4, 0, 0, 1, float("nan"), None) == 1
+    assert call(arr, aux, 2, 2, 4, 0, 0, 2, 0.0, None) == 2
+    assert lib.dq_last_error() == b"fused prologues handle M = 1, got M=2"
+    aux[1] = 0x2008
+    assert call(arr, aux, 2, 1, 4, 0, 0, 2, 0.0, None) == 1
+    assert lib.dq_last_error() == b"problem 1: aux must be 16-byte aligned"
+    aux[1] = None
+    assert call(arr, aux, 2, 1, 4, 0, 0, 2, 0.0, None) == 1
+    assert lib.dq_last_error() == b"problem 1: aux must not be NULL"
+    aux[1] = 0x2000
+    arr[0].K = 250
+    assert call(arr, aux, 2, 1, 4, 0, 0, 1, 1e-5, None) == 1
+    assert lib.dq_last_error() == b"problem 0: K=250 is not divisible by group_size=128"

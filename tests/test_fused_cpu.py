@@ -1,0 +1,55 @@
+"""fuse_llama's module surgery (CPU: no kernel runs). Which layers it fuses,
+what it leaves alone, and that the fused modules keep the quantized buffers."""
+
+import pytest
+import torch
+
+from dequant_project_amd.fused import _DeferredNorm, _FusedMLP, _FusedProjection, fuse_llama
+from dequant_project_amd.packer import QuantConfig
+from dequant_project_amd.quant_linear import QuantLinear, quantize_model
+
+transformers = pytest.importorskip("transformers")
+
+
+def tiny(act="silu", layers=2):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(hidden_size=128, intermediate_size=384, num_hidden_layers=layers, num_attention_heads=4,
+                      num_key_value_heads=2, vocab_size=300, max_position_embeddings=64, hidden_act=act)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg).half().eval()
+
+
+def test_fuses_every_layer_of_a_quantized_llama():
+    model = tiny()
+    quantize_model(model, QuantConfig(4, 128, False))
+    before = {k: v.clone() for k, v in model.state_dict().items()}
+    assert fuse_llama(model) == {"attention": 2, "mlp": 2}
+    for layer in model.model.layers:
+        assert isinstance(layer.input_layernorm, _DeferredNorm)
+        assert isinstance(layer.post_attention_layernorm, _DeferredNorm)
+        assert isinstance(layer.mlp, _FusedMLP)
+        for role in ("q_proj", "k_proj", "v_proj"):
+            proj = getattr(layer.self_attn, role)
+            assert isinstance(proj, _FusedProjection) and isinstance(proj.linear, QuantLinear)
+        assert isinstance(layer.self_attn.o_proj, QuantLinear)
+    # the packed buffers are the same tensors, now under the wrappers' names
+    after = model.state_dict()
+    for k, v in before.items():
+        k2 = (k.replace("q_proj.", "q_proj.linear.").replace("k_proj.", "k_proj.linear.")
+              .replace("v_proj.", "v_proj.linear.").replace("layernorm.", "layernorm.norm.")
+              .replace(".mlp.", ".mlp.mlp."))
+        assert torch.equal(after[k2], v), k
+
+
+def test_leaves_unfusable_layers_alone():
+    plain = tiny()
+    assert fuse_llama(plain) == {"attention": 0, "mlp": 0}      # nothing quantized
+    gelu = tiny(act="gelu")
+    quantize_model(gelu, QuantConfig(8, None, True))
+    assert fuse_llama(gelu) == {"attention": 2, "mlp": 0}        # SwiGLU prologue needs SiLU
+    mixed = tiny()
+    quantize_model(mixed, QuantConfig(4, 128, False))
+    mixed.model.layers[0].self_attn.k_proj = QuantLinear.from_linear(
+        torch.nn.Linear(128, 64, bias=False).half(), QuantConfig(8, None, True))
+    assert fuse_llama(mixed) == {"attention": 1, "mlp": 2}       # q|k|v must share one format
