@@ -132,10 +132,7 @@ class Engine:
         fmt = f"{cfg.bits}, {str(cfg.symmetric).lower()}, {str(cfg.layout == 'interleaved').lower()}"
         if kind.value == 1:
             return f"gemv_quad_kernel<{fmt}, {rows.value // 4}, {1 if m <= 4 else 2}>", tuple(wk)
-        if kind.value in (2, 3):
-            return f"gemv_m1_kernel<{fmt}, {rows.value}, {'true' if kind.value == 3 else 'false'}>", tuple(wk)
-        mt = 2 if m == 2 else (4 if m <= 4 else 8)
-        return f"gemv_kernel<{fmt}, {mt}, {rows.value}, 1>", tuple(wk)
+        return f"gemv_m1_kernel<{fmt}, {rows.value}, {'true' if kind.value == 3 else 'false'}>", tuple(wk)
 
 
 def build_stack(torch, layers, seed=20251201, cfg=None):

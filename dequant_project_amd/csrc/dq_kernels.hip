@@ -8,8 +8,12 @@
 //   [N, K/group_size]; groups run along K.
 //
 // What replaces what (reference kernels/dequant_gemv.cu):
-//   gemv_kernel        <- gemv_kernel<BITS,SYM,INTER,MT>       :144-217
-//   dequantize_kernel  <- dequantize_kernel<BITS,SYM,INTER>    :113-140
+//   gemv_m1_kernel     <- gemv_kernel<BITS,SYM,INTER,MT>, MT = 1   :144-217
+//   gemv_quad_kernel   <- gemv_kernel<BITS,SYM,INTER,MT>, MT = 8   :144-217
+//                         (2 <= M <= 8)
+//   dequantize_kernel  <- dequantize_kernel<BITS,SYM,INTER>        :113-140
+//   gemm_mfma_kernel   (new: the M > 8 product of quant_linear.py:131-132,
+//                      dequantize + F.linear, in one pass for M <= 64)
 //   unpack_kernel      (new: exposes the unpack step for bit-exact checks)
 //   add_one_kernel     <- kernels/smoke.cu:9-13
 //
@@ -18,12 +22,11 @@
 //     call is a list of one; q|k|v or gate|up of a decoder layer share one
 //     launch). Work is cut into tiles of R rows; a 256-thread block holds
 //     4/wk tiles and the wk waves of a tile split its K range, meeting in LDS.
-//   * Lane l walks the 16-byte chunks cb + l + 64t of its rows, so every
-//     global_load_dwordx4 of a wave reads 1 KiB of one row contiguously. A
-//     chunk holds 128/BITS codes of one group (group_size % (128/BITS) == 0).
-//     Every weight, scale and zero load of up to CMAX chunk columns is issued
-//     before any math (R*CMAX 16-byte loads in flight per lane); with M = 1
-//     the activations of those columns are gathered up front too.
+//   * M = 1: lane l walks the 16-byte chunks cb + l + 64t of its rows, so
+//     every global_load_dwordx4 of a wave reads 1 KiB of one row
+//     contiguously. A chunk holds 128/BITS codes of one group
+//     (group_size % (128/BITS) == 0). Each batch issues the activations, then
+//     every zero, scale and weight load of its R rows, before any math.
 //   * Unpack to exact fp16 (code - zero) pairs in two VALU ops per pair:
 //       v_and_or_b32  (w & mask) | 0x64006400  -> fp16 (1024 + q * 2^p) in both
 //                     halves (q sits in mantissa bits [p, p+BITS), p <= 8);
@@ -31,10 +34,12 @@
 //     (INT8 builds the 0x64qq halves with one v_perm_b32 instead.) Pair i holds
 //     the word's slots (i, i + PER/2); the activations are gathered into the
 //     same pair order, so sequential and interleaved layouts cost the same.
-//   * v_dot2_f32_f16 multiplies a (q - z) pair with an activation pair and
-//     accumulates in fp32; per chunk, acc * scale is added in fp32 -- the
-//     reference's arithmetic (fp32 accumulation of exact (q - z) * x products,
-//     factorized scale), so the reference's elementwise fp32 error bound holds.
+//   * v_dot2_f32_f16 (or, for INT2, the diagonal of v_mfma_f32_4x4x4_16b_f16)
+//     multiplies (q - z) pairs with activation pairs and accumulates in fp32;
+//     per chunk, acc * scale is added in fp32 -- the reference's arithmetic
+//     (fp32 accumulation of exact (q - z) * x products, factorized scale), so
+//     the reference's elementwise fp32 error bound holds. 2 <= M <= 8 runs
+//     the same arithmetic on the matrix cores (gemv_quad_kernel).
 //   * Zero points outside [-1024, 1024] (possible: the packer stores them
 //     unclamped) cannot use the exact fp16 form; such chunks take q exactly and
 //     subtract z * sum(x) in fp32 instead (uniform branch, rare).
@@ -294,33 +299,7 @@ struct TileLoads {
   uint32_t z[CMAX][R];
 };
 
-template <int BITS, bool SYM, int R, int CMAX>
-__device__ __forceinline__ void issue_tile(const KernelProblem& d, const TilePos& t, int lane,
-                                           TileLoads<BITS, R, CMAX>& L) {
-  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
-  const uint32_t meta_row_bytes = static_cast<uint32_t>(d.n_groups) * 2;
-  const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
-  const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row_bytes);
-  const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row_bytes);
-#pragma unroll
-  for (int ct = 0; ct < CMAX; ++ct) {
-    // lanes past the share read zeros (weights, scale and zero): their terms
-    // vanish because their activations are zero too
-    const int c = t.cb + lane + 64 * ct;
-    const uint32_t woff = column_offset(c, t.ce, 16u);
-    const uint32_t moff = c < t.ce ? group_of(d, c) * 2u : kOutOfRange;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t row = static_cast<uint32_t>(min(t.row0 + r, d.N - 1));  // past N: re-read N-1, never stored
-      // weights are read exactly once: stream them past the caches (slc)
-      L.w[ct][r] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, woff, row * row_bytes, 2);
-      L.s[ct][r] = __builtin_amdgcn_raw_buffer_load_b16(sbuf, moff, row * meta_row_bytes, 0);
-      L.z[ct][r] = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, row * meta_row_bytes, 0);
-    }
-  }
-}
-
-// issue_tile for the M = 1 kernel (CMAX = 1): zero points first, then scales,
+// The loads of one M = 1 tile batch: zero points first, then scales,
 // then weights. vmcnt retires in issue order, so the zero-point range check
 // that picks the code path waits only for the small loads, and the math of
 // row r starts as soon as weight row r has arrived.
@@ -445,86 +424,27 @@ __device__ __forceinline__ void x_pairs_pro(XRaw<BITS, PRO>& R, h2 (&xr)[4][Fmt<
   for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(R.x + j * (F::PER / 2), xr[j]);
 }
 
-// The math of one tile for one batch row m: yacc[r] gets sum over the wave's
-// chunks of scale * sum((q - z) x).
-template <int BITS, bool SYM, bool INTER, int R, int CMAX>
-__device__ __forceinline__ void tile_math(const TilePos& t, int lane, const TileLoads<BITS, R, CMAX>& L,
-                                          const h2 (&xr)[CMAX][4][Fmt<BITS>::PAIRS], uint32_t magic,
-                                          float (&yacc)[R]) {
-  using F = Fmt<BITS>;
-  h2 pow_scale[F::NCLS];
-#pragma unroll
-  for (int c = 0; c < F::NCLS; ++c)
-    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
-  const h2 ones = splat(static_cast<_Float16>(1.0f));
-#pragma unroll
-  for (int ct = 0; ct < CMAX; ++ct) {
-    {  // columns past the share hold zeros and add nothing
-      h2 off[R][F::NCLS];
-      bool any_inexact = false;
-#pragma unroll
-      for (int r = 0; r < R; ++r) any_inexact |= !class_offsets<BITS, SYM>(static_cast<uint16_t>(L.z[ct][r]), off[r]);
-      // uniform over the active lanes: does any need sum(x)? (out-of-range zero points)
-      const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
-      float acc[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = 0.f;
-      float xsum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (need_xsum) {
-#pragma unroll
-          for (int i = 0; i < F::PAIRS; ++i) xsum = __builtin_amdgcn_fdot2(xr[ct][j][i], ones, xsum, false);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          uint32_t mp[F::PAIRS];
-          magic_pairs<BITS>(L.w[ct][r][j], magic, mp);
-#pragma unroll
-          for (int i = 0; i < F::PAIRS; ++i) {
-            const h2 d2 = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[r][F::cls(i)]);
-            acc[r] = __builtin_amdgcn_fdot2(d2, xr[ct][j][i], acc[r], false);
-          }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float u = acc[r];
-        if (need_xsum && (L.z[ct][r] & 0x7FFFu) > 0x6400u)
-          u = __builtin_fmaf(-f16_to_f32(static_cast<uint16_t>(L.z[ct][r])), xsum, u);
-        yacc[r] = __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(L.s[ct][r])), u, yacc[r]);
-      }
-    }
-  }
-}
-
-// Reduce the R (x MT) per-lane partial sums of a tile and store y. Block-wide
-// LDS combine when the tile's K is split over wk > 1 waves (`part` is this
+// Reduce the R per-lane partial sums of a tile and store y. Block-wide LDS
+// combine when the tile's K is split over wk > 1 waves (`part` is this
 // iteration's half of a double buffer, so one barrier per tile suffices).
-template <int R, int MT>
-__device__ __forceinline__ void finish_tile(const KernelProblem& d, const TilePos& t, int wave, int lane, int M,
-                                            float (&yacc)[R][MT], float (*part)[R * MT]) {
-  wave_sum_lane63<R * MT>(&yacc[0][0]);
+template <int R>
+__device__ __forceinline__ void finish_tile(const KernelProblem& d, const TilePos& t, int wave, int lane,
+                                            float (&yacc)[R], float (*part)[R]) {
+  wave_sum_lane63<R>(yacc);
   if (t.wk == 1) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-        if (t.active && lane == 63 && t.row0 + r < d.N && (MT == 1 || m < M))
-          d.y[static_cast<int64_t>(m) * d.N + t.row0 + r] = f32_to_f16_rn(yacc[r][m]);
+      if (t.active && lane == 63 && t.row0 + r < d.N) d.y[t.row0 + r] = f32_to_f16_rn(yacc[r]);
   } else {
     if (lane == 63) {
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) part[wave][r * MT + m] = yacc[r][m];
+      for (int r = 0; r < R; ++r) part[wave][r] = yacc[r];
     }
     __syncthreads();  // all 4 waves of the block run the same block-tile sequence
-    if (t.active && t.kw == 0 && lane < R * MT) {
+    if (t.active && t.kw == 0 && lane < R) {
       float v = 0.f;
       for (int j = 0; j < t.wk; ++j) v += part[wave + j][lane];
-      const int r = lane / MT, m = lane - (lane / MT) * MT;
-      if (t.row0 + r < d.N && m < M) d.y[static_cast<int64_t>(m) * d.N + t.row0 + r] = f32_to_f16_rn(v);
+      if (t.row0 + lane < d.N) d.y[t.row0 + lane] = f32_to_f16_rn(v);
     }
   }
 }
@@ -683,10 +603,10 @@ __device__ __forceinline__ float inv_rms(float ssq, int K, float eps) {
 
 template <int R>
 __device__ __forceinline__ void finish_tile_rms(const KernelProblem& d, const TilePos& t, int wave, int lane, float eps,
-                                                float (&yacc)[R][1], float ssq, float (*part)[R + 1]) {
+                                                const float (&yacc)[R], float ssq, float (*part)[R + 1]) {
   float v[R + 1];
 #pragma unroll
-  for (int r = 0; r < R; ++r) v[r] = yacc[r][0];
+  for (int r = 0; r < R; ++r) v[r] = yacc[r];
   v[R] = ssq;
   wave_sum_lane63<R + 1>(v);
   if (t.wk == 1) {
@@ -726,9 +646,9 @@ gemv_m1_kernel(const KernelBatch b) {
   for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
     const TilePos t = locate(b, bt, wave, R, p);
     const KernelProblem& d = b.p[t.p];
-    float yacc[R][1];
+    float yacc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) yacc[r][0] = 0.f;
+    for (int r = 0; r < R; ++r) yacc[r] = 0.f;
     float ssq = 0.f;  // RMSNorm prologue: this wave's sum(x^2)
     if (t.active) {
       // the batch loop is branch-free; a batch with a zero point outside
@@ -763,12 +683,12 @@ gemv_m1_kernel(const KernelBatch b) {
         for (int r = 0; r < R; ++r) acc[r] = 0.f;
         tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr, magic, lane, acc);
 #pragma unroll
-        for (int r = 0; r < R; ++r) yacc[r][0] += acc[r];
+        for (int r = 0; r < R; ++r) yacc[r] += acc[r];
       }
       if (!SYM && __builtin_amdgcn_ballot_w64(wide) != 0) {
         // rare: recompute the whole tile with z * sum(x) for the wide zero points
 #pragma unroll
-        for (int r = 0; r < R; ++r) yacc[r][0] = 0.f;
+        for (int r = 0; r < R; ++r) yacc[r] = 0.f;
         for (int cbase = t.cb; cbase < t.ce; cbase += 64) {
           TilePos tb = t;
           tb.cb = cbase;
@@ -776,319 +696,15 @@ gemv_m1_kernel(const KernelBatch b) {
           float acc[R];
           tile_math_m1_wide_zeros<BITS, INTER, R, MF, PRO>(d, tb, lane, magic, acc);
 #pragma unroll
-          for (int r = 0; r < R; ++r) yacc[r][0] += acc[r];
+          for (int r = 0; r < R; ++r) yacc[r] += acc[r];
         }
       }
     }
     if constexpr (PRO == kProRmsNorm)
       finish_tile_rms<R>(d, t, wave, lane, b.eps, yacc, ssq, part[phase]);
     else
-      finish_tile<R, 1>(d, t, wave, lane, b.M, yacc, part[phase]);
+      finish_tile<R>(d, t, wave, lane, yacc, part[phase]);
     if (t.wk > 1) phase ^= 1;
-  }
-}
-
-// ------------------------------------------------ gemv, general M (fallback)
-// Persistent blocks walk the block-tiles bt = blockIdx.x + k * gridDim.x (the
-// grid is sized to the co-resident blocks). Each block-tile gives each wave
-// one tile (R rows x its share of K): every weight/scale/zero load of that
-// tile is issued before its math, and the activations of the wave's chunk
-// columns are gathered per batch row; latency is hidden by the other
-// resident waves.
-template <int BITS, bool SYM, bool INTER, int MT, int R, int CMAX>
-__global__ void __launch_bounds__(kGemvThreads)
-gemv_kernel(const KernelBatch b) {
-  using F = Fmt<BITS>;
-  // wave-uniform by construction; readfirstlane lets the compiler keep every
-  // derived offset in SGPRs (buffer-load soffset) instead of looping
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int lane = threadIdx.x & 63;
-  __shared__ float part[2][kWavesPerBlock][R * MT];
-  const uint32_t magic = magic_vgpr();
-  const int total = b.bt_start[b.count];
-  int phase = 0;
-  int p = 0;
-  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
-    const TilePos t = locate(b, bt, wave, R, p);
-    const KernelProblem& d = b.p[t.p];
-    float yacc[R][MT];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int m = 0; m < MT; ++m) yacc[r][m] = 0.f;
-    if (t.active) {
-      // the wave's share of K in batches of 64 * CMAX chunks (one 16-byte
-      // column per lane per batch and CMAX)
-      for (int cbase = t.cb; cbase < t.ce; cbase += 64 * CMAX) {
-        TilePos tb = t;
-        tb.cb = cbase;
-        tb.ce = min(t.ce, cbase + 64 * CMAX);
-        TileLoads<BITS, R, CMAX> L;
-        issue_tile<BITS, SYM, R, CMAX>(d, tb, lane, L);
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          if (m < b.M) {
-            h2 xr[CMAX][4][F::PAIRS];
-            load_x_columns<BITS, INTER, CMAX>(d, tb, lane, m, xr);
-            float acc[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = 0.f;
-            tile_math<BITS, SYM, INTER, R, CMAX>(tb, lane, L, xr, magic, acc);
-#pragma unroll
-            for (int r = 0; r < R; ++r) yacc[r][m] += acc[r];
-          }
-        }
-      }
-    }
-    finish_tile<R, MT>(d, t, wave, lane, b.M, yacc, part[phase]);
-    // the LDS half flips only on tiles that used it (those end with a block
-    // barrier), so a half is rewritten only after every wave has passed the
-    // barrier that follows its last read
-    if (t.wk > 1) phase ^= 1;
-  }
-}
-
-// ------------------------------------------------------ gemv, 2 <= M <= 8 (MFMA)
-// Batch rows share every weight, so for M > 1 the products go to the matrix
-// cores: v_mfma_f32_16x16x32_f16 with the activations as the A operand
-// (16 x 32: rows m, K) and the exact (q - z) weights as the B operand
-// (32 x 16: K, output columns n). Lane l = (kb = l/16, r = l%16):
-//   A  x[min(r, M-1)][8 codes of chunk 4t + kb]       (8 halves)
-//   B  (q - z) of row n = row0 + 16 rb + r, same 8 codes of chunk 4t + kb
-//   D  lane l holds D[m = 4 kb + i][n = r], i = 0..3
-// so one MFMA reduces 32 codes (4 lanes x 8) of 16 rows for all M rows, and
-// the unpack, the group scale (fp32, per lane: the lane's own row) and the
-// (rare) out-of-range-zero correction are the VALU work. An iteration t covers
-// chunks 4t..4t+3 of each row, i.e. 4 * (128/BITS) codes, which must lie in
-// one group: group_size % (4 * 128/BITS) == 0 (the host checks and otherwise
-// uses gemv_kernel). The loads of iteration t+1 are issued before the math of
-// iteration t (two register sets).
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-
-struct MfmaProblem {
-  const uint32_t* qweight;
-  const uint16_t* scales;
-  const uint16_t* zeros;
-  const uint16_t* x;
-  uint16_t* y;
-  int N, K;
-  int n_groups;   // K / group_size
-  int ipg;        // iterations per group: group_size / (4 * 128/BITS)
-  int ipg_shift;  // log2(ipg) when a power of two, else -1
-  int n_iters;    // K / (4 * 128/BITS)
-  int lwk;        // log2 of the waves sharing one tile along K
-  int per_wave;   // ceil(n_iters / wk)
-  int tiles;      // ceil(N / (16 * RB))
-};
-
-struct MfmaBatch {
-  MfmaProblem p[kMaxBatch];
-  int bt_start[kMaxBatch + 1];
-  int count;
-  int M;
-};
-
-template <int BITS, int RB>
-struct MfmaLoads {
-  u32x4 w[RB];
-  uint32_t s[RB];  // fp16 bit patterns, zero-extended (see TileLoads)
-  uint32_t z[RB];
-  u32x4 x[Fmt<BITS>::CPL / 8];
-};
-
-struct MfmaAddr {
-  __amdgpu_buffer_rsrc_t wbuf, sbuf, zbuf, xbuf;
-  uint32_t wv[4], mv[4];  // per-lane row offsets (weights, scales/zeros)
-  uint32_t xv;            // per-lane activation offset
-};
-
-__device__ __forceinline__ h8 pack8(h2 a, h2 b, h2 c, h2 d) {
-  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-  const h4 lo = __builtin_shufflevector(a, b, 0, 1, 2, 3);
-  const h4 hi = __builtin_shufflevector(c, d, 0, 1, 2, 3);
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-template <int BITS, bool SYM, int RB>
-__device__ __forceinline__ void mfma_issue(const MfmaProblem& d, const MfmaAddr& a, int t, MfmaLoads<BITS, RB>& L) {
-  constexpr int CPL = Fmt<BITS>::CPL;
-  const int g = d.n_groups == 1 ? 0 : (d.ipg_shift >= 0 ? t >> d.ipg_shift : t / d.ipg);
-  const uint32_t wso = static_cast<uint32_t>(t) * 64u;
-  const uint32_t mso = static_cast<uint32_t>(g) * 2u;
-  const uint32_t xso = static_cast<uint32_t>(t) * (4u * CPL * 2u);
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    L.w[rb] = __builtin_amdgcn_raw_buffer_load_b128(a.wbuf, a.wv[rb], wso, 2);
-    L.s[rb] = __builtin_amdgcn_raw_buffer_load_b16(a.sbuf, a.mv[rb], mso, 0);
-    L.z[rb] = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(a.zbuf, a.mv[rb], mso, 0);
-  }
-#pragma unroll
-  for (int q = 0; q < CPL / 8; ++q) L.x[q] = __builtin_amdgcn_raw_buffer_load_b128(a.xbuf, a.xv + 16u * q, xso, 0);
-}
-
-// One iteration: yacc[rb][i] += scale * sum over the iteration's codes.
-template <int BITS, bool SYM, bool INTER, int RB>
-__device__ __forceinline__ void mfma_math(const MfmaLoads<BITS, RB>& L, uint32_t magic, float (&yacc)[RB][4]) {
-  using F = Fmt<BITS>;
-  constexpr int CPL = F::CPL, NMF = CPL / 8, NP = CPL / 2;
-  uint32_t xd[CPL / 2];
-#pragma unroll
-  for (int q = 0; q < CPL / 8; ++q)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) xd[4 * q + e] = L.x[q][e];
-  h2 xp[NP];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp + j * F::PAIRS);
-  h8 xa[NMF];
-#pragma unroll
-  for (int f = 0; f < NMF; ++f) xa[f] = pack8(xp[4 * f], xp[4 * f + 1], xp[4 * f + 2], xp[4 * f + 3]);
-  h2 pow_scale[F::NCLS];
-#pragma unroll
-  for (int c = 0; c < F::NCLS; ++c)
-    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
-  h2 off[RB][F::NCLS];
-  bool any_inexact = false;
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) any_inexact |= !class_offsets<BITS, SYM>(static_cast<uint16_t>(L.z[rb]), off[rb]);
-  // sum(x) per batch row, only when some zero point is outside [-1024, 1024]
-  const bool need_xsum = !SYM && __builtin_amdgcn_ballot_w64(any_inexact) != 0;
-  f4 xsum = {0.f, 0.f, 0.f, 0.f};
-  if (need_xsum) {
-    const h2 one = splat(static_cast<_Float16>(1.0f));
-    const h8 ones = pack8(one, one, one, one);
-#pragma unroll
-    for (int f = 0; f < NMF; ++f) xsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[f], ones, xsum, 0, 0, 0);
-  }
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    h2 dq2[NP];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t mp[F::PAIRS];
-      magic_pairs<BITS>(L.w[rb][j], magic, mp);
-#pragma unroll
-      for (int i = 0; i < F::PAIRS; ++i)
-        dq2[j * F::PAIRS + i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[rb][F::cls(i)]);
-    }
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int f = 0; f < NMF; ++f)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          xa[f], pack8(dq2[4 * f], dq2[4 * f + 1], dq2[4 * f + 2], dq2[4 * f + 3]), acc, 0, 0, 0);
-    if (need_xsum && (L.z[rb] & 0x7FFFu) > 0x6400u) {
-      const float z = f16_to_f32(static_cast<uint16_t>(L.z[rb]));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(-z, xsum[i], acc[i]);
-    }
-    const float s = f16_to_f32(static_cast<uint16_t>(L.s[rb]));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) yacc[rb][i] = __builtin_fmaf(s, acc[i], yacc[rb][i]);
-  }
-}
-
-// Persistent blocks walk block-tiles like gemv_kernel; a tile is 16 * RB rows
-// and the wk waves of a tile split its iterations, meeting in LDS.
-template <int BITS, bool SYM, bool INTER, int RB>
-__global__ void __launch_bounds__(kGemvThreads) gemv_mfma_kernel(const MfmaBatch b) {
-  using F = Fmt<BITS>;
-  constexpr int CPL = F::CPL;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int lane = threadIdx.x & 63;
-  const int r = lane & 15, kb = lane >> 4;
-  // partial sums of lanes 0..31 (batch rows 0..7) per wave, double-buffered
-  __shared__ float part[2][kWavesPerBlock * RB * 4 * 32];
-  const uint32_t magic = magic_vgpr();
-  const int total = b.bt_start[b.count];
-  int phase = 0;
-  int p = 0;
-  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
-    while (p + 1 < b.count && bt >= b.bt_start[p + 1]) ++p;
-    const MfmaProblem& d = b.p[p];
-    const int wk = 1 << d.lwk;
-    const int slot = wave >> d.lwk;
-    const int kw = wave & (wk - 1);
-    const int tile = ((bt - b.bt_start[p]) << (2 - d.lwk)) + slot;
-    const bool active = tile < d.tiles;
-    const int row0 = tile * 16 * RB;
-    const int ib = kw * d.per_wave;
-    const int ie = min(d.n_iters, ib + d.per_wave);
-    float yacc[RB][4];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) yacc[rb][i] = 0.f;
-    if (active && ib < ie) {
-      MfmaAddr a;
-      const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
-      const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
-      a.wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
-      a.sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row);
-      a.zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row);
-      a.xbuf = buffer_of(d.x, static_cast<uint32_t>(b.M) * static_cast<uint32_t>(d.K) * 2u);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const uint32_t n = static_cast<uint32_t>(min(row0 + 16 * rb + r, d.N - 1));  // past N: re-read, never stored
-        a.wv[rb] = n * row_bytes + 16u * kb;
-        a.mv[rb] = n * meta_row;
-      }
-      a.xv = static_cast<uint32_t>(min(r, b.M - 1)) * static_cast<uint32_t>(d.K) * 2u +
-             static_cast<uint32_t>(kb) * (CPL * 2u);
-      // two register sets: loads of the next iteration fly during this one's math
-      MfmaLoads<BITS, RB> A, B;
-      mfma_issue<BITS, SYM, RB>(d, a, ib, A);
-      int t = ib;
-      while (true) {
-        if (t + 1 >= ie) {
-          mfma_math<BITS, SYM, INTER, RB>(A, magic, yacc);
-          break;
-        }
-        mfma_issue<BITS, SYM, RB>(d, a, t + 1, B);
-        mfma_math<BITS, SYM, INTER, RB>(A, magic, yacc);
-        ++t;
-        if (t + 1 >= ie) {
-          mfma_math<BITS, SYM, INTER, RB>(B, magic, yacc);
-          break;
-        }
-        mfma_issue<BITS, SYM, RB>(d, a, t + 1, A);
-        mfma_math<BITS, SYM, INTER, RB>(B, magic, yacc);
-        ++t;
-      }
-    }
-    // lanes 0..31 hold batch rows m = 4 kb + i (< 8) of column n = row0 + 16 rb + r
-    if (wk == 1) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const int n = row0 + 16 * rb + r;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 4 * kb + i;
-          if (active && kb < 2 && m < b.M && n < d.N) d.y[static_cast<int64_t>(m) * d.N + n] = f32_to_f16_rn(yacc[rb][i]);
-        }
-      }
-    } else {
-      float* pp = part[phase];
-      if (lane < 32) {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) pp[((wave * RB + rb) * 4 + i) * 32 + lane] = yacc[rb][i];
-      }
-      __syncthreads();  // all 4 waves of the block run the same block-tile sequence
-      if (active && kw == 0 && lane < 32) {
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          const int n = row0 + 16 * rb + r;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v = 0.f;
-            for (int j = 0; j < wk; ++j) v += pp[(((wave + j) * RB + rb) * 4 + i) * 32 + lane];
-            const int m = 4 * kb + i;
-            if (m < b.M && n < d.N) d.y[static_cast<int64_t>(m) * d.N + n] = f32_to_f16_rn(v);
-          }
-        }
-      }
-      phase ^= 1;  // same rule as gemv_kernel: only tiles that used the LDS flip it
-    }
   }
 }
 
@@ -1331,6 +947,15 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
       phase ^= 1;
     }
   }
+}
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ h8 pack8(h2 a, h2 b, h2 c, h2 d) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 lo = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+  const h4 hi = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // ---------------------------------------------------- small GEMM, M <= 64 (MFMA)
@@ -1643,8 +1268,6 @@ int64_t elementwise_blocks(int64_t items) {
 // Geometry changes only the order of fp32 additions (split-K partial sums),
 // so a problem's result is deterministic for a given launch but may differ in
 // the last bits between a grouped launch and a single one.
-constexpr int kCmax = 1;
-
 // M = 1 dot products on the matrix cores (gemv_m1_kernel<..., MF = true)?
 // Measured on the Llama-3-8B stack shapes (8-row tiles): INT2 g64 48.3% of
 // peak with MFMA vs 46.1% on the VALU (its 16 codes per word make v_dot2 the
@@ -1656,8 +1279,7 @@ constexpr int64_t kMinColumns = 40;
 
 int64_t target_waves(int bits) { return bits == 8 ? 8192 : (bits == 4 ? 6144 : 4096); }
 
-int rows_per_tile(const GemvOperand* ops, int count, int64_t M) {
-  if (M > 1) return 1;
+int rows_per_tile(const GemvOperand* ops, int count) {
   int64_t tiles8 = 0;
   for (int i = 0; i < count; ++i) tiles8 += (ops[i].N + 7) / 8;
   return tiles8 >= kWideTiles ? 8 : 4;
@@ -1763,22 +1385,16 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
   return bts;
 }
 
-template <int BITS, bool SYM, bool INTER, int MT, int R, int PRO = kProNone>
-hipError_t launch_gemv_r(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
+template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
+hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
   int wks[kMaxBatch];
   waves_per_tile(ops, count, BITS, R, wks);
   KernelBatch kb;
   const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
   kb.eps = eps;
   if (bts == 0) return hipSuccess;
-  if constexpr (MT == 1) {
-    constexpr bool MF = m1_uses_mfma(BITS);
-    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, MF, PRO>;
-    return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
-  } else {
-    constexpr auto kernel = gemv_kernel<BITS, SYM, INTER, MT, R, kCmax>;
-    return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
-  }
+  constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO>;
+  return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
 }
 
 // Geometry of the quad kernel (2 <= M <= 8): tiles of 4 * kQuadsPerTile rows,
@@ -1796,71 +1412,6 @@ hipError_t launch_gemv_quad(const GemvOperand* ops, int count, int64_t M, hipStr
   if (bts == 0) return hipSuccess;
   constexpr auto kernel = gemv_quad_kernel<BITS, SYM, INTER, kQuadsPerTile, MG>;
   return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
-}
-
-// Geometry of the MFMA kernel (2 <= M <= 8):
-//   RB   16-row blocks per tile: 4 when the launch has at least 400 tiles of
-//        64 rows, 2 when it has at least 800 of 32, else 1 (small launches
-//        need the waves more than the reuse of the activation operand).
-//   wk   per problem, waves sharing a tile along K: the fewest of {1, 2, 4}
-//        that leave each wave at most 8 iterations.
-bool mfma_applies(const GemvOperand* ops, int count, int64_t M, int bits) {
-  if (M < 2) return false;
-  const int64_t span = 4 * (128 / bits);  // codes per iteration
-  for (int i = 0; i < count; ++i)
-    if (ops[i].group_size % span != 0) return false;
-  return true;
-}
-
-int mfma_row_blocks(const GemvOperand* ops, int count) {
-  int64_t t4 = 0, t2 = 0;
-  for (int i = 0; i < count; ++i) {
-    t4 += (ops[i].N + 63) / 64;
-    t2 += (ops[i].N + 31) / 32;
-  }
-  return t4 >= 400 ? 4 : (t2 >= 800 ? 2 : 1);
-}
-
-int mfma_waves_per_tile(int64_t K, int bits) {
-  const int64_t iters = K / (4 * (128 / bits));
-  int wk = 1;
-  while (wk < 4 && (iters + wk - 1) / wk > 8) wk *= 2;
-  return wk;
-}
-
-template <int BITS, bool SYM, bool INTER, int RB>
-hipError_t launch_gemv_mfma(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
-  constexpr int SPAN = 4 * (128 / BITS);
-  MfmaBatch mb{};
-  mb.count = count;
-  mb.M = static_cast<int>(M);
-  int bts = 0;
-  for (int i = 0; i < count; ++i) {
-    const GemvOperand& o = ops[i];
-    MfmaProblem& k = mb.p[i];
-    k.qweight = o.qweight;
-    k.scales = o.scales;
-    k.zeros = o.zeros;
-    k.x = o.x;
-    k.y = o.y;
-    k.N = static_cast<int>(o.N);
-    k.K = static_cast<int>(o.K);
-    k.n_groups = static_cast<int>(o.K / o.group_size);
-    k.ipg = static_cast<int>(o.group_size / SPAN);
-    k.ipg_shift = log2_exact(k.ipg);
-    k.n_iters = static_cast<int>(o.K / SPAN);
-    const int wk = mfma_waves_per_tile(o.K, BITS);
-    k.lwk = log2_exact(wk);
-    k.per_wave = (k.n_iters + wk - 1) / wk;
-    k.tiles = static_cast<int>((o.N + 16 * RB - 1) / (16 * RB));
-    const int tiles_per_bt = kWavesPerBlock / wk;
-    mb.bt_start[i] = bts;
-    bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
-  }
-  mb.bt_start[count] = bts;
-  if (bts == 0) return hipSuccess;
-  constexpr auto kernel = gemv_mfma_kernel<BITS, SYM, INTER, RB>;
-  return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), mb, stream);
 }
 
 // Geometry of the small GEMM (8 < M <= 64, or any M <= 64 the caller sends):
@@ -1939,8 +1490,8 @@ hipError_t launch_gemm_t(const GemvOperand* ops, int count, int64_t M, hipStream
 template <int BITS, bool SYM, bool INTER>
 hipError_t launch_gemv_t(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
   if (M == 1) {
-    if (rows_per_tile(ops, count, M) == 8) return launch_gemv_r<BITS, SYM, INTER, 1, 8>(ops, count, M, stream);
-    return launch_gemv_r<BITS, SYM, INTER, 1, 4>(ops, count, M, stream);
+    if (rows_per_tile(ops, count) == 8) return launch_gemv_m1<BITS, SYM, INTER, 8>(ops, count, M, stream);
+    return launch_gemv_m1<BITS, SYM, INTER, 4>(ops, count, M, stream);
   }
   if (M <= 4) return launch_gemv_quad<BITS, SYM, INTER, 1>(ops, count, M, stream);
   return launch_gemv_quad<BITS, SYM, INTER, 2>(ops, count, M, stream);
@@ -1950,13 +1501,13 @@ template <int BITS, bool SYM, bool INTER>
 hipError_t launch_gemv_prologue_t(const GemvOperand* ops, int count, int64_t M, int prologue, float eps,
                                   hipStream_t stream) {
   if (M != 1) return hipErrorInvalidValue;
-  const bool wide_tiles = rows_per_tile(ops, count, M) == 8;
+  const bool wide_tiles = rows_per_tile(ops, count) == 8;
   if (prologue == kPrologueRmsNorm)
-    return wide_tiles ? launch_gemv_r<BITS, SYM, INTER, 1, 8, kProRmsNorm>(ops, count, M, stream, eps)
-                      : launch_gemv_r<BITS, SYM, INTER, 1, 4, kProRmsNorm>(ops, count, M, stream, eps);
+    return wide_tiles ? launch_gemv_m1<BITS, SYM, INTER, 8, kProRmsNorm>(ops, count, M, stream, eps)
+                      : launch_gemv_m1<BITS, SYM, INTER, 4, kProRmsNorm>(ops, count, M, stream, eps);
   if (prologue == kPrologueSwiGlu)
-    return wide_tiles ? launch_gemv_r<BITS, SYM, INTER, 1, 8, kProSwiGlu>(ops, count, M, stream)
-                      : launch_gemv_r<BITS, SYM, INTER, 1, 4, kProSwiGlu>(ops, count, M, stream);
+    return wide_tiles ? launch_gemv_m1<BITS, SYM, INTER, 8, kProSwiGlu>(ops, count, M, stream)
+                      : launch_gemv_m1<BITS, SYM, INTER, 4, kProSwiGlu>(ops, count, M, stream);
   return hipErrorInvalidValue;
 }
 
@@ -2013,7 +1564,7 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
     return;
   }
   *mfma = M == 1 ? (m1_uses_mfma(bits) ? 3 : 2) : 0;
-  *rows = rows_per_tile(ops, count, M);
+  *rows = rows_per_tile(ops, count);
   waves_per_tile(ops, count, bits, *rows, wk);
 }
 
