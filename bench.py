@@ -36,6 +36,10 @@ Printed: ONE JSON line on stdout (progress goes to stderr).
               layer of the same stack, on this host's cores
   other_format_stacks / batch_stacks  the same stack step in INT8 and INT2,
               and the INT4 stack at M = 2, 4, 8 (C4's other batch sizes)
+  gemm_small_stacks  the fused small GEMM over the stack at M = 16, 64, with
+              the reference's dequantize + F.linear timed beside it
+  decode_with_fused_prologues  the decode launches with RMSNorm / SwiGLU
+              fused in, against the same launches without
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 100]
 """
@@ -320,6 +324,85 @@ def single_config(torch, eng, name, n, k, cfg, m, reps=10):
     return name, res
 
 
+def gemm_stack(torch, stack, m, steps, warmup):
+    """The fused small GEMM (quant_linear.gemm_small) over every projection of
+    the stack at m rows (a prefill chunk through all layers), in one graph,
+    against the reference's M > 8 path (dequantize + F.linear) timed eagerly
+    with HIP events (each of its GEMMs is tens of microseconds)."""
+    import torch.nn.functional as F
+
+    from dequant_project_amd.quant_linear import dequantize_cuda, gemm_small
+
+    gen = torch.Generator(device="cuda").manual_seed(20251204 + m)
+    xs = {k: torch.randn(m, k, generator=gen, device="cuda", dtype=torch.float16) for k in (HIDDEN, INTER)}
+    items = [(xs[p.shape[1]], p) for layer in stack for _, p in sorted(layer.items())]
+    step_bytes = sum(launch_bytes([x], [p]) for x, p in items)
+
+    def fused():
+        for x, p in items:
+            gemm_small(x, p)
+
+    graph = capture(torch, fused)
+    ms, per = time_graph(torch, graph, steps, warmup)
+    del graph
+
+    def reference():
+        for x, p in items:
+            F.linear(x, dequantize_cuda(p))
+
+    reference()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ref = []
+    for _ in range(max(3, steps // 4)):
+        a.record()
+        reference()
+        b.record()
+        torch.cuda.synchronize()
+        ref.append(a.elapsed_time(b))
+    ref_ms = statistics.median(ref)
+    return {"M": m, "bytes_per_step": step_bytes, "ms_per_step": ms, "step_ms": summarize(per),
+            "gbs": step_bytes / (ms * 1e-3) / 1e9, "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+            "us_per_layer": ms * 1e3 / len(stack),
+            "dequantize_plus_linear_ms_per_step": ref_ms, "speedup_vs_dequantize_plus_linear": ref_ms / ms}
+
+
+def prologue_decode(torch, eng, stack, xs, steps, warmup):
+    """The decode launch structure (q|k|v, o, gate|up, down per layer) with the
+    RMSNorm prologue fused into q|k|v and gate|up and the SwiGLU prologue into
+    down (fused.gemv_rmsnorm / gemv_swiglu), against the same launches without
+    prologues: what the fusion costs inside the GEMVs (the separate norm and
+    SwiGLU kernels it removes are not counted here)."""
+    from dequant_project_amd import fused
+
+    gen = torch.Generator(device="cuda").manual_seed(20251205)
+    gamma = torch.rand(HIDDEN, generator=gen, device="cuda", dtype=torch.float16) + 0.5
+    ups = [torch.randn(1, INTER, generator=gen, device="cuda", dtype=torch.float16) for _ in stack]
+    plain = step_launches(stack, xs, "decode")
+    step_bytes = sum(launch_bytes(x, p) for _, x, p in plain)
+
+    def run_plain():
+        for _, x, p in plain:
+            eng.gemv_group(x, p)
+
+    def run_fused():
+        for li, (layer, x) in enumerate(zip(stack, xs)):
+            fused.gemv_rmsnorm(x["qkv"], gamma, 1e-5, [layer["q_proj"], layer["k_proj"], layer["v_proj"]])
+            eng.gemv_group([x["o"]], [layer["o_proj"]])
+            fused.gemv_rmsnorm(x["gate_up"], gamma, 1e-5, [layer["gate_proj"], layer["up_proj"]])
+            fused.gemv_swiglu(x["down"], ups[li], layer["down_proj"])
+
+    out = {}
+    for name, fn in (("plain", run_plain), ("fused_prologues", run_fused)):
+        graph = capture(torch, fn)
+        ms, per = time_graph(torch, graph, steps, warmup)
+        del graph
+        out[name] = {"ms_per_step": ms, "step_ms": summarize(per), "us_per_layer": ms * 1e3 / len(stack),
+                     "gbs": step_bytes / (ms * 1e-3) / 1e9}
+    out["bytes_per_step"] = step_bytes
+    return out
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_m1_kernel_int4_c4_stack_traffic.md")
 
 
@@ -443,6 +526,21 @@ def main():
                 f"{batch_stacks[f'M={m}']['us_per_layer']:.2f} us/layer")
             del mxs, launches
 
+    # the fused small GEMM over the stack (M > 8: the reference's dequantize +
+    # F.linear path) and the decode launches with fused prologues
+    gemm = {}
+    prologue = None
+    if not args.no_extra:
+        for m in (16, 64):
+            gemm[f"M={m}"] = gemm_stack(torch, stack, m, args.steps, args.warmup // 4)
+            g = gemm[f"M={m}"]
+            log(f"gemm_small stack M={m}: {g['ms_per_step']:.3f} ms/step  {g['gbs']:.1f} GB/s  "
+                f"(dequantize + F.linear {g['dequantize_plus_linear_ms_per_step']:.3f} ms/step, "
+                f"{g['speedup_vs_dequantize_plus_linear']:.2f}x)")
+        prologue = prologue_decode(torch, eng, stack, xs, args.steps, args.warmup)
+        log(f"decode launches: plain {prologue['plain']['us_per_layer']:.2f} us/layer, with fused prologues "
+            f"{prologue['fused_prologues']['us_per_layer']:.2f} us/layer")
+
     extra = {}
     if not args.no_extra:
         for name, n, k, c, m in [("C1", 4096, 4096, QuantConfig(4, 128, False), 1),
@@ -478,6 +576,8 @@ def main():
         "modes": modes,
         "other_format_stacks": other_stacks,
         "batch_stacks": batch_stacks,
+        "gemm_small_stacks": gemm,
+        "decode_with_fused_prologues": prologue,
         "single_configs": extra,
     }
     print(json.dumps(line, default=lambda o: sorted(o) if isinstance(o, set) else str(o)), flush=True)

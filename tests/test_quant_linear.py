@@ -25,7 +25,7 @@ from torch import nn
 
 from dequant_project_amd import packer
 from dequant_project_amd.packer import QuantConfig, quantize_tensor
-from dequant_project_amd.quant_linear import MAX_M, MAX_M_GEMM, PROJ, QuantLinear, quantize_model
+from dequant_project_amd.quant_linear import MAX_M, PROJ, QuantLinear, quantize_model, uses_gemm_small
 from oracle import packer_ref as P
 
 
@@ -177,7 +177,7 @@ def test_quant_linear_against_f_linear(torch_gpu, shape):
     xf = x.float().reshape(m, k)
     ref = xf @ w_ref.T + ql.bias.float()
     absref = xf.abs() @ w_ref.abs().T
-    path = "gemv" if m <= MAX_M else ("gemm_small" if m <= MAX_M_GEMM else "fallback")
+    path = "gemv" if m <= MAX_M else ("gemm_small" if uses_gemm_small(m, n, k) else "fallback")
     _check(y.reshape(m, n), ref, absref, 2, f"QuantLinear {shape} M={m} via {path}")
 
 
