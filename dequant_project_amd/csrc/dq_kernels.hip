@@ -729,17 +729,70 @@ gemv_m1_kernel(const KernelBatch b) {
 // Zero points outside [-1024, 1024] (WIDE, rare, asymmetric only): the tile
 // is recomputed with q alone for those rows and z * sum(x) subtracted in fp32,
 // sum(x) per chunk and batch row from one more MFMA chain against ones.
-template <int BITS, bool SYM, bool INTER, int NT, int MG, bool WIDE>
+// Activations of one k-step for the whole block, staged in LDS: each step the
+// block loads, for each of its wk K-shares, the 16 chunks of x the step
+// covers (4*MG batch rows; one coalesced 16-byte piece per lane and load),
+// and every wave reads its A fragments from there. Without the staging each
+// wave loaded its own copy per step: as many bytes as its weights (M <= 4,
+// INT4), and the load-class ablation put that at a third of the kernel's time.
+// Double-buffered by step parity, one barrier per step. Rows are padded by 16
+// bytes so the 16-byte fragment reads of a lane quad hit distinct banks.
+template <int BITS, int MG, int WK>
+struct QuadStage {
+  static constexpr int kChunkBytes = Fmt<BITS>::CPL * 2;          // one row's activations of one chunk
+  static constexpr int kPieces = kChunkBytes / 16;                  // 16-byte pieces per chunk
+  static constexpr int kRowBytes = 16 * kChunkBytes + 16;          // one row's 16 chunks, padded
+  static constexpr int kRows = 4 * MG;
+  static constexpr int kBufBytes = WK * kRows * kRowBytes;
+  static constexpr int kTotal = WK * kRows * 16 * kPieces;          // pieces per step
+  static constexpr int kPerLane = (kTotal + kGemvThreads - 1) / kGemvThreads;
+};
+
+template <int BITS, int MG, int WK>
+__device__ __forceinline__ void stage_issue(const KernelProblem& d, int M, int s, u32x4 (&st)[QuadStage<BITS, MG, WK>::kPerLane]) {
+  using QS = QuadStage<BITS, MG, WK>;
+  const uint32_t kb = static_cast<uint32_t>(d.K) * 2u;
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(M) * kb);
+#pragma unroll
+  for (int i = 0; i < QS::kPerLane; ++i) {
+    const int e = static_cast<int>(threadIdx.x) + kGemvThreads * i;
+    const int piece = e % QS::kPieces, cl = (e / QS::kPieces) % 16, r = e / (QS::kPieces * 16);
+    const int m = r % QS::kRows, j = r / QS::kRows;
+    const int c = j * d.per_wave + 16 * s + cl;
+    const bool ok = e < QS::kTotal && m < M && c < min(d.n_chunks, (j + 1) * d.per_wave);
+    st[i] = __builtin_amdgcn_raw_buffer_load_b128(
+        xbuf, ok ? static_cast<uint32_t>(m) * kb + static_cast<uint32_t>(c) * QS::kChunkBytes + 16u * piece
+                 : kOutOfRange,
+        0, 0);
+  }
+}
+
+template <int BITS, int MG, int WK>
+__device__ __forceinline__ void stage_write(unsigned char* buf, const u32x4 (&st)[QuadStage<BITS, MG, WK>::kPerLane]) {
+  using QS = QuadStage<BITS, MG, WK>;
+#pragma unroll
+  for (int i = 0; i < QS::kPerLane; ++i) {
+    const int e = static_cast<int>(threadIdx.x) + kGemvThreads * i;
+    const int piece = e % QS::kPieces, cl = (e / QS::kPieces) % 16, r = e / (QS::kPieces * 16);
+    if (e < QS::kTotal)
+      *reinterpret_cast<u32x4*>(buf + r * QS::kRowBytes + cl * QS::kChunkBytes + 16 * piece) = st[i];
+  }
+}
+
+// One tile (4 * NT rows x the wave's K-share) of the quad kernel. Every wave
+// of the block runs the same number of steps (inactive waves with no loads of
+// their own) so that all take part in the staging and its barriers.
+template <int BITS, bool SYM, bool INTER, int NT, int MG, int WK, bool WIDE>
 __device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos& t, int M, int blk, int q,
-                                          uint32_t magic, f4 (&acc)[NT][MG], bool& wide) {
+                                          uint32_t magic, unsigned char* lds, f4 (&acc)[NT][MG], bool& wide) {
   using F = Fmt<BITS>;
+  using QS = QuadStage<BITS, MG, WK>;
   constexpr int CPL = F::CPL, NF = CPL / 4;
   const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
   const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
   const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
   const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row);
   const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row);
-  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(M) * static_cast<uint32_t>(d.K) * 2u);
   uint32_t wrow[NT], mrow[NT];
 #pragma unroll
   for (int g = 0; g < NT; ++g) {
@@ -747,20 +800,18 @@ __device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos&
     wrow[g] = n * row_bytes;
     mrow[g] = n * meta_row;
   }
-  uint32_t xrow[MG];
-  bool xok[MG];
-#pragma unroll
-  for (int mg = 0; mg < MG; ++mg) {
-    xok[mg] = 4 * mg + q < M;
-    xrow[mg] = static_cast<uint32_t>(4 * mg + q) * static_cast<uint32_t>(d.K) * 2u;
-  }
   h2 pow_scale[F::NCLS];
 #pragma unroll
   for (int c = 0; c < F::NCLS; ++c)
     pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
-  for (int cs = t.cb; cs < t.ce; cs += 16) {
-    const int c = cs + blk;
-    const bool ok = c < t.ce;
+  const int nsteps = d.per_wave >> 4;
+  for (int s = 0; s < nsteps; ++s) {
+    unsigned char* buf = lds + (s & 1) * QS::kBufBytes;
+    // activations first: the LDS write below waits for them, not for the weights
+    u32x4 st[QS::kPerLane];
+    stage_issue<BITS, MG, WK>(d, M, s, st);
+    const int c = t.cb + 16 * s + blk;
+    const bool ok = t.active && c < t.ce;
     const uint32_t gmo = ok ? group_of(d, c) * 2u : 0u;
     uint32_t zb[NT], sb[NT];
     u32x4 w[NT];
@@ -774,14 +825,16 @@ __device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos&
     for (int g = 0; g < NT; ++g)
       w[g] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, ok ? wrow[g] + static_cast<uint32_t>(c) * 16u : kOutOfRange,
                                                    0, 2);
+    __builtin_amdgcn_sched_barrier(0);  // every global load of the step is in flight before the staging waits
+    stage_write<BITS, MG, WK>(buf, st);
+    __syncthreads();
     u32x4 xv[MG][CPL / 8];
 #pragma unroll
     for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
       for (int k = 0; k < CPL / 8; ++k)
-        xv[mg][k] = __builtin_amdgcn_raw_buffer_load_b128(
-            xbuf, ok && xok[mg] ? xrow[mg] + static_cast<uint32_t>(c) * (CPL * 2u) + 16u * k : kOutOfRange, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);  // every load of the step is in flight before the math
+        xv[mg][k] = *reinterpret_cast<const u32x4*>(buf + (t.kw * QS::kRows + 4 * mg + q) * QS::kRowBytes +
+                                                     blk * QS::kChunkBytes + 16 * k);
     h2 xp[MG][CPL / 2];
 #pragma unroll
     for (int mg = 0; mg < MG; ++mg) {
@@ -838,7 +891,7 @@ __device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos&
         for (int i = 0; i < F::PAIRS; ++i)
           dq[j * F::PAIRS + i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]);
       }
-      const float s = f16_to_f32(static_cast<uint16_t>(sb[g]));
+      const float sc = f16_to_f32(static_cast<uint16_t>(sb[g]));
 #pragma unroll
       for (int mg = 0; mg < MG; ++mg) {
         f4 D = {0.f, 0.f, 0.f, 0.f};
@@ -852,7 +905,7 @@ __device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos&
           for (int i = 0; i < 4; ++i) D[i] = __builtin_fmaf(-zf, xs[mg][i], D[i]);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[g][mg][i] = __builtin_fmaf(s, D[i], acc[g][mg][i]);
+        for (int i = 0; i < 4; ++i) acc[g][mg][i] = __builtin_fmaf(sc, D[i], acc[g][mg][i]);
       }
     }
   }
@@ -881,15 +934,19 @@ __device__ __forceinline__ float quad_column_sum(float v) {
   return swap_sum32(swap_sum16(v));
 }
 
-// Persistent blocks walk block-tiles like gemv_kernel; a tile is 4 * NT rows
-// and the wk waves of a tile split its chunks (in steps of 16), meeting in LDS.
-template <int BITS, bool SYM, bool INTER, int NT, int MG>
+// Persistent blocks walk block-tiles like the M = 1 kernel; a tile is 4 * NT
+// rows and the WK waves of a tile split its chunks (in steps of 16), meeting
+// in LDS. Every problem of a launch uses WK waves per tile (the staging layout
+// holds WK K-shares).
+template <int BITS, bool SYM, bool INTER, int NT, int MG, int WK>
 __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBatch b) {
+  using QS = QuadStage<BITS, MG, WK>;
   constexpr int NV = NT * MG * 4;  // outputs of one column q per tile: (g, mg, i)
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int blk = lane >> 2, q = lane & 3;
   __shared__ float part[2][kWavesPerBlock][NV][4];
+  __shared__ __align__(16) unsigned char xlds[2 * QS::kBufBytes];
   const uint32_t magic = magic_vgpr();
   const int total = b.bt_start[b.count];
   int phase = 0;
@@ -902,16 +959,15 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
     for (int g = 0; g < NT; ++g)
 #pragma unroll
       for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
-    if (t.active && t.cb < t.ce) {
-      bool wide = false;
-      quad_tile<BITS, SYM, INTER, NT, MG, false>(d, t, b.M, blk, q, magic, acc, wide);
-      if (!SYM && __builtin_amdgcn_ballot_w64(wide) != 0) {
+    // every wave of the block, active or not, runs the steps (they stage x together)
+    bool wide = false;
+    quad_tile<BITS, SYM, INTER, NT, MG, WK, false>(d, t, b.M, blk, q, magic, xlds, acc, wide);
+    if (!SYM && __syncthreads_or(wide)) {
 #pragma unroll
-        for (int g = 0; g < NT; ++g)
+      for (int g = 0; g < NT; ++g)
 #pragma unroll
-          for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
-        quad_tile<BITS, SYM, INTER, NT, MG, true>(d, t, b.M, blk, q, magic, acc, wide);
-      }
+        for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
+      quad_tile<BITS, SYM, INTER, NT, MG, WK, true>(d, t, b.M, blk, q, magic, xlds, acc, wide);
     }
     float tot[NV];
 #pragma unroll
@@ -1399,19 +1455,40 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
 
 // Geometry of the quad kernel (2 <= M <= 8): tiles of 4 * kQuadsPerTile rows,
 // MG = 1 batch-row group of 4 for M <= 4, else 2; wk as for the M = 1 kernel
-// (tiles of 16 rows), each wave's share rounded up to whole steps of 16 chunks.
+// (tiles of 16 rows), the same for every problem of the launch (the smallest
+// of the problems' choices; capped at 2 for INT2 with MG = 2, whose staging
+// buffers would otherwise take 132 KiB of LDS), each wave's share rounded up
+// to whole steps of 16 chunks.
 constexpr int kQuadsPerTile = 4;
 
-template <int BITS, bool SYM, bool INTER, int MG>
-hipError_t launch_gemv_quad(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+int quad_waves_per_tile(const GemvOperand* ops, int count, int bits, int mg) {
+  int wks[kMaxBatch];
+  waves_per_tile(ops, count, bits, 4 * kQuadsPerTile, wks);
+  int wk = 4;
+  for (int i = 0; i < count; ++i) wk = std::min(wk, wks[i]);
+  if (bits == 2 && mg == 2) wk = std::min(wk, 2);
+  return wk;
+}
+
+template <int BITS, bool SYM, bool INTER, int MG, int WK>
+hipError_t launch_gemv_quad_wk(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
   constexpr int R = 4 * kQuadsPerTile;
   int wks[kMaxBatch];
-  waves_per_tile(ops, count, BITS, R, wks);
+  for (int i = 0; i < count; ++i) wks[i] = WK;
   KernelBatch kb;
   const int bts = fill_kernel_batch(ops, count, M, BITS, R, 16, wks, kb);
   if (bts == 0) return hipSuccess;
-  constexpr auto kernel = gemv_quad_kernel<BITS, SYM, INTER, kQuadsPerTile, MG>;
+  constexpr auto kernel = gemv_quad_kernel<BITS, SYM, INTER, kQuadsPerTile, MG, WK>;
   return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+}
+
+template <int BITS, bool SYM, bool INTER, int MG>
+hipError_t launch_gemv_quad(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
+  const int wk = quad_waves_per_tile(ops, count, BITS, MG);
+  if (wk == 1) return launch_gemv_quad_wk<BITS, SYM, INTER, MG, 1>(ops, count, M, stream);
+  if (wk == 2) return launch_gemv_quad_wk<BITS, SYM, INTER, MG, 2>(ops, count, M, stream);
+  if constexpr (BITS == 2 && MG == 2) return hipErrorInvalidValue;  // capped above
+  else return launch_gemv_quad_wk<BITS, SYM, INTER, MG, 4>(ops, count, M, stream);
 }
 
 // Geometry of the small GEMM (8 < M <= 64, or any M <= 64 the caller sends):
@@ -1560,7 +1637,8 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
   if (M >= 2) {
     *mfma = 1;
     *rows = 4 * kQuadsPerTile;
-    waves_per_tile(ops, count, bits, *rows, wk);
+    const int w = quad_waves_per_tile(ops, count, bits, M <= 4 ? 1 : 2);
+    for (int i = 0; i < count; ++i) wk[i] = w;
     return;
   }
   *mfma = M == 1 ? (m1_uses_mfma(bits) ? 3 : 2) : 0;
