@@ -427,14 +427,36 @@ __device__ __forceinline__ void x_pairs_pro(XRaw<BITS, PRO>& R, h2 (&xr)[4][Fmt<
 // Reduce the R per-lane partial sums of a tile and store y. Block-wide LDS
 // combine when the tile's K is split over wk > 1 waves (`part` is this
 // iteration's half of a double buffer, so one barrier per tile suffices).
+// The R consecutive outputs of a tile held by one lane, stored with one
+// 8- or 16-byte store when the tile is whole and y is aligned for it (one
+// memory instruction instead of R two-byte stores from a single lane: those
+// were a third of the M = 1 kernel's memory instructions on 2 KiB rows).
+template <int R>
+__device__ __forceinline__ void store_row_block(uint16_t* y, int row0, int N, const float (&v)[R]) {
+  static_assert(R == 4 || R == 8, "rows per tile");
+  uint16_t* dst = y + row0;
+  if (row0 + R <= N && (reinterpret_cast<uintptr_t>(dst) & (2 * R - 1)) == 0) {
+    uint32_t w[R / 2];
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i)
+      w[i] = static_cast<uint32_t>(f32_to_f16_rn(v[2 * i])) | (static_cast<uint32_t>(f32_to_f16_rn(v[2 * i + 1])) << 16);
+    if constexpr (R == 8)
+      *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+    else
+      *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (row0 + r < N) dst[r] = f32_to_f16_rn(v[r]);
+  }
+}
+
 template <int R>
 __device__ __forceinline__ void finish_tile(const KernelProblem& d, const TilePos& t, int wave, int lane,
                                             float (&yacc)[R], float (*part)[R]) {
   wave_sum_lane63<R>(yacc);
   if (t.wk == 1) {
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (t.active && lane == 63 && t.row0 + r < d.N) d.y[t.row0 + r] = f32_to_f16_rn(yacc[r]);
+    if (t.active && lane == 63) store_row_block<R>(d.y, t.row0, d.N, yacc);
   } else {
     if (lane == 63) {
 #pragma unroll
@@ -611,9 +633,10 @@ __device__ __forceinline__ void finish_tile_rms(const KernelProblem& d, const Ti
   wave_sum_lane63<R + 1>(v);
   if (t.wk == 1) {
     const float f = inv_rms(v[R], d.K, eps);
+    float o[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (t.active && lane == 63 && t.row0 + r < d.N) d.y[t.row0 + r] = f32_to_f16_rn(v[r] * f);
+    for (int r = 0; r < R; ++r) o[r] = v[r] * f;
+    if (t.active && lane == 63) store_row_block<R>(d.y, t.row0, d.N, o);
   } else {
     if (lane == 63) {
 #pragma unroll
