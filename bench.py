@@ -40,6 +40,9 @@ Printed: ONE JSON line on stdout (progress goes to stderr).
               the reference's dequantize + F.linear timed beside it
   decode_with_fused_prologues  the decode launches with RMSNorm / SwiGLU
               fused in, against the same launches without
+  c5_llama3_70b_stack  BASELINE.json's C5: the Llama-3-70B shapes, INT4
+              attention, INT2 MLP, INT8 lm_head (~25 GB), stack and decode
+              launch structures
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 100]
 """
@@ -403,6 +406,79 @@ def prologue_decode(torch, eng, stack, xs, steps, warmup):
     return out
 
 
+# a Llama-3-70B-shape stack in mixed precision
+C5_LAYERS = 80
+C5_HIDDEN, C5_KV, C5_INTER, C5_VOCAB = 8192, 1024, 28672, 128256
+
+
+def c5_stack(torch, eng, steps, warmup, layers=C5_LAYERS):
+    """80 layers of q/k/v/o in INT4 g128 asym and gate/up/down in INT2 g64
+    asym, plus an INT8 per-channel sym lm_head 8192 -> 128256 (~25 GB
+    packed), from seeded fp16 N(0, 0.02) weights quantized on the GPU one
+    tensor at a time; x fp16 N(0, 1), batch 1. Timed as grouped launches of
+    equal format and K ("stack") and as a decoder launches them ("decode":
+    q|k|v, o, gate|up, down per layer, then the lm_head)."""
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    attn, mlp, head = QuantConfig(4, 128, False), QuantConfig(2, 64, False), QuantConfig(8, None, True)
+    gen = torch.Generator(device="cuda").manual_seed(20251206)
+
+    def q(n, k, cfg):
+        w = torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02
+        pw = quantize_tensor(w, cfg)
+        del w
+        return pw
+
+    t0 = time.perf_counter()
+    stack = []
+    for _ in range(layers):
+        stack.append({"q_proj": q(C5_HIDDEN, C5_HIDDEN, attn), "k_proj": q(C5_KV, C5_HIDDEN, attn),
+                      "v_proj": q(C5_KV, C5_HIDDEN, attn), "o_proj": q(C5_HIDDEN, C5_HIDDEN, attn),
+                      "gate_proj": q(C5_INTER, C5_HIDDEN, mlp), "up_proj": q(C5_INTER, C5_HIDDEN, mlp),
+                      "down_proj": q(C5_HIDDEN, C5_INTER, mlp)})
+    lm_head = q(C5_VOCAB, C5_HIDDEN, head)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    xs = [{"qkv": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+           "o": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+           "gate_up": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+           "down": torch.randn(1, C5_INTER, generator=gen, device="cuda", dtype=torch.float16)} for _ in stack]
+    x_head = torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16)
+
+    launches = {}
+    groups = {}
+    for layer, x in zip(stack, xs):
+        for role, names in GROUPS:
+            for n in names:
+                p = layer[n]
+                groups.setdefault((p.config.bits, p.shape[1]), []).append((x[role], p))
+    launches["stack"] = [([c[0] for c in items[i:i + 16]], [c[1] for c in items[i:i + 16]])
+                         for items in groups.values() for i in range(0, len(items), 16)]
+    launches["decode"] = [([x[role]] * len(names), [layer[n] for n in names])
+                          for layer, x in zip(stack, xs) for role, names in GROUPS]
+    for mode in launches:
+        launches[mode].append(([x_head], [lm_head]))
+    out = {"layers": layers, "build_s": build_s}
+    for mode, ls in launches.items():
+        step_bytes = sum(launch_bytes(x, p) for x, p in ls)
+
+        def fn():
+            for x, p in ls:
+                eng.gemv_group(x, p)
+
+        graph = capture(torch, fn)
+        ms, per = time_graph(torch, graph, steps, warmup)
+        del graph
+        out[mode] = {"launches_per_step": len(ls), "bytes_per_step": step_bytes, "ms_per_step": ms,
+                     "step_ms": summarize(per), "gbs": step_bytes / (ms * 1e-3) / 1e9,
+                     "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
+                     "us_per_layer": ms * 1e3 / layers,
+                     "kernel_instances": {k: len(v) for k, v in kernel_instances(eng, [(None, x, p) for x, p in ls]).items()}}
+    del stack, lm_head, launches, groups
+    torch.cuda.empty_cache()
+    return out
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_m1_kernel_int4_c4_stack_traffic.md")
 
 
@@ -541,6 +617,14 @@ def main():
         log(f"decode launches: plain {prologue['plain']['us_per_layer']:.2f} us/layer, with fused prologues "
             f"{prologue['fused_prologues']['us_per_layer']:.2f} us/layer")
 
+    c5 = None
+    if not args.no_extra:
+        c5 = c5_stack(torch, eng, args.steps, args.warmup // 4)
+        log(f"C5 (Llama-3-70B shapes, INT4 attention / INT2 MLP / INT8 lm_head, {c5['stack']['bytes_per_step'] / 1e9:.2f} GB,"
+            f" built in {c5['build_s']:.0f}s): stack {c5['stack']['ms_per_step']:.3f} ms/step "
+            f"{c5['stack']['gbs']:.1f} GB/s {c5['stack']['us_per_layer']:.2f} us/layer; decode "
+            f"{c5['decode']['ms_per_step']:.3f} ms/step {c5['decode']['gbs']:.1f} GB/s")
+
     extra = {}
     if not args.no_extra:
         for name, n, k, c, m in [("C1", 4096, 4096, QuantConfig(4, 128, False), 1),
@@ -578,6 +662,7 @@ def main():
         "batch_stacks": batch_stacks,
         "gemm_small_stacks": gemm,
         "decode_with_fused_prologues": prologue,
+        "c5_llama3_70b_stack": c5,
         "single_configs": extra,
     }
     print(json.dumps(line, default=lambda o: sorted(o) if isinstance(o, set) else str(o)), flush=True)
