@@ -805,9 +805,14 @@ __device__ __forceinline__ void stage_write(unsigned char* buf, const u32x4 (&st
 // One tile (4 * NT rows x the wave's K-share) of the quad kernel. Every wave
 // of the block runs the same number of steps (inactive waves with no loads of
 // their own) so that all take part in the staging and its barriers.
+// `parity` selects the staging buffer of the next step; it runs on across
+// tiles, so consecutive steps of a block always alternate buffers (a tile's
+// first step must not overwrite the buffer the previous tile's last step may
+// still be reading).
 template <int BITS, bool SYM, bool INTER, int NT, int MG, int WK, bool WIDE>
 __device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos& t, int M, int blk, int q,
-                                          uint32_t magic, unsigned char* lds, f4 (&acc)[NT][MG], bool& wide) {
+                                          uint32_t magic, unsigned char* lds, int& parity, f4 (&acc)[NT][MG],
+                                          bool& wide) {
   using F = Fmt<BITS>;
   using QS = QuadStage<BITS, MG, WK>;
   constexpr int CPL = F::CPL, NF = CPL / 4;
@@ -829,7 +834,8 @@ __device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos&
     pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
   const int nsteps = d.per_wave >> 4;
   for (int s = 0; s < nsteps; ++s) {
-    unsigned char* buf = lds + (s & 1) * QS::kBufBytes;
+    unsigned char* buf = lds + parity * QS::kBufBytes;
+    parity ^= 1;
     // activations first: the LDS write below waits for them, not for the weights
     u32x4 st[QS::kPerLane];
     stage_issue<BITS, MG, WK>(d, M, s, st);
@@ -973,6 +979,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
   const uint32_t magic = magic_vgpr();
   const int total = b.bt_start[b.count];
   int phase = 0;
+  int parity = 0;  // staging buffer of the next step
   int p = 0;
   for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
     const TilePos t = locate(b, bt, wave, 4 * NT, p);
@@ -984,13 +991,13 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
       for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
     // every wave of the block, active or not, runs the steps (they stage x together)
     bool wide = false;
-    quad_tile<BITS, SYM, INTER, NT, MG, WK, false>(d, t, b.M, blk, q, magic, xlds, acc, wide);
+    quad_tile<BITS, SYM, INTER, NT, MG, WK, false>(d, t, b.M, blk, q, magic, xlds, parity, acc, wide);
     if (!SYM && __syncthreads_or(wide)) {
 #pragma unroll
       for (int g = 0; g < NT; ++g)
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
-      quad_tile<BITS, SYM, INTER, NT, MG, WK, true>(d, t, b.M, blk, q, magic, xlds, acc, wide);
+      quad_tile<BITS, SYM, INTER, NT, MG, WK, true>(d, t, b.M, blk, q, magic, xlds, parity, acc, wide);
     }
     float tot[NV];
 #pragma unroll
