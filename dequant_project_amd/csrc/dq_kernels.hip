@@ -300,9 +300,8 @@ struct TileLoads {
 };
 
 // The loads of one M = 1 tile batch: zero points first, then scales,
-// then weights. vmcnt retires in issue order, so the zero-point range check
-// that picks the code path waits only for the small loads, and the math of
-// row r starts as soon as weight row r has arrived.
+// then weights. vmcnt retires in issue order, so the math of row r starts as
+// soon as weight row r has arrived.
 template <int BITS, bool SYM, int R>
 __device__ __forceinline__ void issue_tile_m1(const KernelProblem& d, const TilePos& t, int lane,
                                               TileLoads<BITS, R, 1>& L) {
@@ -473,62 +472,146 @@ __device__ __forceinline__ void finish_tile(const KernelProblem& d, const TilePo
 
 // ------------------------------------------------------------- gemv, M = 1
 // The M = 1 hot path. Same tile walk and loads as gemv_kernel, with the math
-// specialized for one activation row:
-//   * the common case (every zero point of the batch within [-1024, 1024])
-//     and the rare one (some zero point outside it, e.g. heavy outliers with
-//     the packer's unclamped zeros) are separate code paths chosen by a
-//     wave-uniform ballot, so the hot loop carries no sum(x) work and no
-//     per-row selects (folding them in as selects cost ~20% more VALU
-//     instructions and registers);
+// specialized for one activation row.
+//
+// Biased codes. A code masked into the mantissa of an fp16 half at bit p,
+// under exponent field 25 - p, reads exactly 2^(10-p) + q (the half's value
+// is 2^(10-p) * (1 + q 2^p / 2^10)); one v_and_or_b32 per pair then makes the
+// fp16 operands and no multiply is needed. The bias and the zero point come
+// off per row and chunk in fp32:
+//   sum_k (q_k - z) x_k = sum_k (bias_k + q_k) x_k - (C + z S),
+//   S = sum_k x_k,  C = sum_k bias_k x_k,
+// with S and C taken once per lane and batch (the activations are shared by
+// the tile's R rows). Every product is exact (fp16 operands, fp32 products)
+// and the sums run in fp32; the bias terms cancel in the subtraction, so the
+// sums' rounding error grows with the bias. The codes are therefore placed as
+// high in the mantissa as one shift per copy of the word allows:
+//   INT4  every nibble at bit 4 (bias 64), from w << 4, w, w >> 4, w >> 8;
+//   INT2  codes at bits 4 / 6 / 8 (bias 64 / 16 / 4), from w << 4, w, w >> 6;
+//   INT8  the byte at bit 0 (bias 1024), by byte permutation.
+// A CPU model of this summation order puts its error at under a quarter of
+// the fp32 budget of the reference's kernel test (2^-20 sum |w||x|, its
+// scripts/test_dequant_kernel.py:112-122; exact (q - z) products: ~1%). The
+// form holds for any zero point (the packer's zeros are unclamped,
+// packer.py:136-137), so there is no separate path for large zero points.
 //   * MF = false: products and sums with v_dot2_f32_f16 (VALU);
 //     MF = true:  the dot products go to the matrix cores. The 64 lanes form
 //     the 16 blocks of v_mfma_f32_4x4x4_16b_f16, four consecutive chunk
 //     columns of one row each; with A = the lane's own activations and B =
-//     its own exact (q - z) codes, register (lane % 4) of the 4x4 result
-//     holds the lane's own dot product (the diagonal), so the load pattern
-//     stays one contiguous 1 KiB row segment per wave and load.
+//     its own biased codes, register (lane % 4) of the 4x4 result holds the
+//     lane's own dot product (the diagonal), so the load pattern stays one
+//     contiguous 1 KiB row segment per wave and load.
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ h4 cat2(h2 a, h2 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3); }
 
-// One row's dot product for the M = 1 kernel: sum over the lane's chunk of
-// (q - z) x, with (q - z) exact in fp16. `zh` is the zero point to subtract
-// (0 when the caller subtracts z * sum(x) itself).
-template <int BITS, bool INTER, bool MF>
-__device__ __forceinline__ float row_dot_m1(const u32x4& w, _Float16 zh, const h2 (&xr)[1][4][Fmt<BITS>::PAIRS],
-                                            uint32_t magic, int lane) {
-  using F = Fmt<BITS>;
-  h2 pow_scale[F::NCLS];
-#pragma unroll
-  for (int c = 0; c < F::NCLS; ++c)
-    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
-  // exact (q - z) = magic * 2^-p - (2^(10-p) + z)
-  const h2 zz = splat(zh);
-  h2 off[F::NCLS];
-#pragma unroll
-  for (int c = 0; c < F::NCLS; c += 2) {
-    const _Float16 b0 = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c))));
-    const _Float16 b1 =
-        c + 1 < F::NCLS ? static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c + 1)))) : b0;
-    const h2 both = -(h2{b0, b1} + zz);  // one v_pk_add_f16 for two classes
-    off[c] = splat(both.x);
-    if (c + 1 < F::NCLS) off[c + 1] = splat(both.y);
+// Pair i of a word holds slots i and i + PER/2 (the pair order of
+// x_pairs_from_dwords); its codes sit at mantissa bit pow(cls(i)).
+template <int BITS> struct Biased {
+  static constexpr int NCLS = BITS == 2 ? 3 : 1;
+  static constexpr __device__ int cls(int i) {
+    if constexpr (BITS == 2) {
+      constexpr int t[8] = {0, 1, 0, 1, 2, 0, 1, 2};
+      return t[i];
+    } else {
+      return 0;
+    }
   }
+  static constexpr int pow(int c) { return BITS == 8 ? 0 : 4 + 2 * c; }
+  static constexpr float bias(int c) { return static_cast<float>(1 << (10 - pow(c))); }
+  static constexpr uint32_t magic(int c) {
+    const uint32_t e = static_cast<uint32_t>(25 - pow(c));
+    return (e << 10) | (e << 26);
+  }
+};
+
+template <uint32_t V>
+__device__ __forceinline__ uint32_t vgpr_const() {
+  uint32_t m;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(m) : "i"(V));
+  return m;
+}
+
+// The class magics held in VGPRs (as magic_vgpr, so that each pair is one
+// v_and_or_b32 with the mask as its one scalar operand).
+template <int BITS>
+struct ClassMagics {
+  uint32_t m[Biased<BITS>::NCLS];
+  __device__ __forceinline__ void init() {
+    m[0] = vgpr_const<Biased<BITS>::magic(0)>();
+    if constexpr (Biased<BITS>::NCLS > 1) m[1] = vgpr_const<Biased<BITS>::magic(1)>();
+    if constexpr (Biased<BITS>::NCLS > 2) m[2] = vgpr_const<Biased<BITS>::magic(2)>();
+  }
+};
+
+// Word -> PER/2 biased pairs: both halves of pair i are bias + q, the low
+// half from slot i, the high half from slot i + PER/2. Each half's codes sit
+// at the same offsets, and no mask reaches bits a shift carried across the
+// halves' boundary.
+template <int BITS>
+__device__ __forceinline__ void biased_pairs(uint32_t w, const ClassMagics<BITS>& cm, uint32_t* p) {
+  if constexpr (BITS == 8) {
+    p[0] = __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u);  // {0x64, b2, 0x64, b0}: 1024 + q
+    p[1] = __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u);
+  } else if constexpr (BITS == 4) {
+    constexpr uint32_t kNib = 0x00F000F0u;  // bits 4-7 of each half
+    p[0] = ((w << 4) & kNib) | cm.m[0];
+    p[1] = (w & kNib) | cm.m[0];
+    p[2] = ((w >> 4) & kNib) | cm.m[0];
+    p[3] = ((w >> 8) & kNib) | cm.m[0];
+  } else {
+    constexpr uint32_t k4 = 0x00300030u, k6 = 0x00C000C0u, k8 = 0x03000300u;
+    const uint32_t wl = w << 4, wr = w >> 6;
+    p[0] = (wl & k4) | cm.m[0];  // slot 0: bit 0 -> 4
+    p[1] = (wl & k6) | cm.m[1];  // slot 1: bit 2 -> 6
+    p[2] = (w & k4) | cm.m[0];   // slot 2: bit 4
+    p[3] = (w & k6) | cm.m[1];   // slot 3: bit 6
+    p[4] = (w & k8) | cm.m[2];   // slot 4: bit 8
+    p[5] = (wr & k4) | cm.m[0];  // slot 5: bit 10 -> 4
+    p[6] = (wr & k6) | cm.m[1];  // slot 6: bit 12 -> 6
+    p[7] = (wr & k8) | cm.m[2];  // slot 7: bit 14 -> 8
+  }
+}
+
+// S = sum(x) and C = sum(bias * x) over the lane's chunk, per class with
+// v_dot2 against ones (exact products, fp32 sums).
+template <int BITS>
+__device__ __forceinline__ void bias_sums(const h2 (&xr)[4][Fmt<BITS>::PAIRS], float& S, float& C) {
+  using F = Fmt<BITS>;
+  using B = Biased<BITS>;
+  const h2 one = splat(static_cast<_Float16>(1.0f));
+  float sc[B::NCLS];
+#pragma unroll
+  for (int c = 0; c < B::NCLS; ++c) sc[c] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < F::PAIRS; ++i) sc[B::cls(i)] = __builtin_amdgcn_fdot2(xr[j][i], one, sc[B::cls(i)], false);
+  S = sc[0];
+  C = B::bias(0) * sc[0];
+#pragma unroll
+  for (int c = 1; c < B::NCLS; ++c) {
+    S += sc[c];
+    C = __builtin_fmaf(B::bias(c), sc[c], C);
+  }
+}
+
+// sum over the lane's chunk of (bias + q) x for one row.
+template <int BITS, bool MF>
+__device__ __forceinline__ float biased_dot_m1(const u32x4& w, const h2 (&xr)[4][Fmt<BITS>::PAIRS],
+                                               const ClassMagics<BITS>& cm, int lane) {
+  using F = Fmt<BITS>;
   if constexpr (MF) {
     f4 D = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t mp[F::PAIRS];
-      magic_pairs<BITS>(w[j], magic, mp);
-      h2 dq[F::PAIRS];
-#pragma unroll
-      for (int i = 0; i < F::PAIRS; ++i)
-        dq[i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]);
+      biased_pairs<BITS>(w[j], cm, mp);
 #pragma unroll
       for (int i = 0; i < F::PAIRS; i += 2)
-        D = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xr[0][j][i], xr[0][j][i + 1]), cat2(dq[i], dq[i + 1]), D, 0, 0,
-                                               0);
+        D = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xr[j][i], xr[j][i + 1]), cat2(as_h2(mp[i]), as_h2(mp[i + 1])), D,
+                                               0, 0, 0);
     }
     const bool s1 = lane & 1, s2 = lane & 2;
     return s2 ? (s1 ? D[3] : D[2]) : (s1 ? D[1] : D[0]);
@@ -537,83 +620,28 @@ __device__ __forceinline__ float row_dot_m1(const u32x4& w, _Float16 zh, const h
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t mp[F::PAIRS];
-      magic_pairs<BITS>(w[j], magic, mp);
+      biased_pairs<BITS>(w[j], cm, mp);
 #pragma unroll
-      for (int i = 0; i < F::PAIRS; ++i) {
-        const h2 d2 = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]);
-        v = __builtin_amdgcn_fdot2(d2, xr[0][j][i], v, false);
-      }
+      for (int i = 0; i < F::PAIRS; ++i) v = __builtin_amdgcn_fdot2(as_h2(mp[i]), xr[j][i], v, false);
     }
     return v;
   }
 }
 
-// Common case: every zero point of the batch is within [-1024, 1024].
+// One batch of a tile: acc[r] = scale_r * (sum (bias + q) x - (C + z_r S)).
 template <int BITS, bool SYM, bool INTER, int R, bool MF>
-__device__ __forceinline__ void tile_math_m1(const TileLoads<BITS, R, 1>& L, const h2 (&xr)[1][4][Fmt<BITS>::PAIRS],
-                                             uint32_t magic, int lane, float (&acc)[R]) {
+__device__ __forceinline__ void tile_math_m1(const TileLoads<BITS, R, 1>& L, const h2 (&xr)[4][Fmt<BITS>::PAIRS],
+                                             const ClassMagics<BITS>& cm, int lane, float (&acc)[R]) {
   using F = Fmt<BITS>;
+  float S, C;
+  bias_sums<BITS>(xr, S, C);
+  if constexpr (SYM) C = __builtin_fmaf(static_cast<float>(F::BIAS), S, C);  // z = 2^(b-1) for every row
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const _Float16 zh = SYM ? static_cast<_Float16>(static_cast<float>(F::BIAS))
-                            : __builtin_bit_cast(_Float16, static_cast<uint16_t>(L.z[0][r]));
-    const float v = row_dot_m1<BITS, INTER, MF>(L.w[0][r], zh, xr, magic, lane);
+    const float corr = SYM ? C : __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(L.z[0][r])), S, C);
+    const float v = biased_dot_m1<BITS, MF>(L.w[0][r], xr, cm, lane) - corr;
     acc[r] = __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(L.s[0][r])), v, acc[r]);
   }
-}
-
-// Rare case (asymmetric only): some zero point of the tile is outside
-// [-1024, 1024] (or not finite), where (q - z) is not exact in fp16. Such rows
-// take q exactly and subtract z * sum(x) in fp32; one call covers one batch. It holds none of the tile's
-// loaded registers: it re-reads the activations, and each row's weights,
-// scale and zero in a rolled loop, so it adds little to the kernel's register
-// budget; results rotate into acc[] in row order.
-template <int BITS, bool INTER, int R, bool MF, int PRO>
-__device__ __forceinline__ void tile_math_m1_wide_zeros(const KernelProblem& d, const TilePos& tb, int lane,
-                                                        uint32_t magic, float (&acc)[R]) {
-  using F = Fmt<BITS>;
-  h2 xr[1][4][F::PAIRS];
-  if constexpr (PRO == kProNone) {
-    load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
-  } else {
-    XRaw<BITS, PRO> raw;
-    issue_x_pro<BITS, PRO>(d, tb, lane, 0, 1, raw);
-    float unused = 0.f;
-    x_pairs_pro<BITS, INTER, PRO>(raw, xr[0], unused);
-  }
-  float xsum = 0.f;
-  const h2 one = splat(static_cast<_Float16>(1.0f));
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < F::PAIRS; ++i) xsum = __builtin_amdgcn_fdot2(xr[0][j][i], one, xsum, false);
-  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
-  const uint32_t meta_row_bytes = static_cast<uint32_t>(d.n_groups) * 2;
-  const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
-  const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row_bytes);
-  const __amdgpu_buffer_rsrc_t zbuf = buffer_of(d.zeros, static_cast<uint32_t>(d.N) * meta_row_bytes);
-  const int c = tb.cb + lane;
-  const uint32_t woff = column_offset(c, tb.ce, 16u);
-  const uint32_t moff = c < tb.ce ? group_of(d, c) * 2u : kOutOfRange;
-  float res[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) res[r] = 0.f;
-#pragma unroll 1
-  for (int r = 0; r < R; ++r) {
-    const uint32_t row = static_cast<uint32_t>(min(tb.row0 + r, d.N - 1));
-    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(wbuf, woff, row * row_bytes, 0);
-    const uint32_t sb = __builtin_amdgcn_raw_buffer_load_b16(sbuf, moff, row * meta_row_bytes, 0);
-    const uint32_t zb = __builtin_amdgcn_raw_buffer_load_b16(zbuf, moff, row * meta_row_bytes, 0);
-    const bool inexact = (zb & 0x7FFFu) > 0x6400u;
-    const _Float16 zh = inexact ? static_cast<_Float16>(0.0f) : __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb));
-    float v = row_dot_m1<BITS, INTER, MF>(w, zh, xr, magic, lane);
-    if (inexact) v = __builtin_fmaf(-f16_to_f32(static_cast<uint16_t>(zb)), xsum, v);
-#pragma unroll
-    for (int i = 0; i + 1 < R; ++i) res[i] = res[i + 1];
-    res[R - 1] = f16_to_f32(static_cast<uint16_t>(sb)) * v;
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = res[r];
 }
 
 // finish_tile for the RMSNorm prologue: the R dot products and the wave's
@@ -662,7 +690,8 @@ gemv_m1_kernel(const KernelBatch b) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   __shared__ float part[2][kWavesPerBlock][PW];
-  const uint32_t magic = magic_vgpr();
+  ClassMagics<BITS> cm;
+  cm.init();
   const int total = b.bt_start[b.count];
   int phase = 0;
   int p = 0;
@@ -674,9 +703,6 @@ gemv_m1_kernel(const KernelBatch b) {
     for (int r = 0; r < R; ++r) yacc[r] = 0.f;
     float ssq = 0.f;  // RMSNorm prologue: this wave's sum(x^2)
     if (t.active) {
-      // the batch loop is branch-free; a batch with a zero point outside
-      // [-1024, 1024] only sets `wide`, and the tile is then redone below
-      bool wide = false;
       for (int cbase = t.cb; cbase < t.ce; cbase += 64) {
         TilePos tb = t;
         tb.cb = cbase;
@@ -697,30 +723,12 @@ gemv_m1_kernel(const KernelBatch b) {
         // leaving one or two rows in flight and the latency exposed per row
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (PRO != kProNone) x_pairs_pro<BITS, INTER, PRO>(raw, xr[0], ssq);
-        if constexpr (!SYM) {
-#pragma unroll
-          for (int r = 0; r < R; ++r) wide |= (L.z[0][r] & 0x7FFFu) > 0x6400u;
-        }
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.f;
-        tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr, magic, lane, acc);
+        tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr[0], cm, lane, acc);
 #pragma unroll
         for (int r = 0; r < R; ++r) yacc[r] += acc[r];
-      }
-      if (!SYM && __builtin_amdgcn_ballot_w64(wide) != 0) {
-        // rare: recompute the whole tile with z * sum(x) for the wide zero points
-#pragma unroll
-        for (int r = 0; r < R; ++r) yacc[r] = 0.f;
-        for (int cbase = t.cb; cbase < t.ce; cbase += 64) {
-          TilePos tb = t;
-          tb.cb = cbase;
-          tb.ce = min(t.ce, cbase + 64);
-          float acc[R];
-          tile_math_m1_wide_zeros<BITS, INTER, R, MF, PRO>(d, tb, lane, magic, acc);
-#pragma unroll
-          for (int r = 0; r < R; ++r) yacc[r] += acc[r];
-        }
       }
     }
     if constexpr (PRO == kProRmsNorm)

@@ -502,10 +502,20 @@ def test_c_abi_matches_extension(torch_gpu):
 
 
 # ------------------------------------------------------- grouped launch
+GROUPED_VS_SINGLE_REL_L2 = 1e-4
+
+
 @pytest.mark.parametrize("m", (1, 3, 8))
 def test_grouped_launch_matches_oracle_and_single_calls(torch_gpu, m):
     """dq_gemv_batched: one launch; every problem within the oracle tolerances,
-    deterministic, and equal to its single call up to split-K fp32 rounding."""
+    deterministic, and equal to its single call up to split-K fp32 rounding.
+
+    GROUPED_VS_SINGLE_REL_L2: a grouped launch may split a tile's K over a
+    different number of waves than the single call, which changes the fp32
+    summation order; the M = 1 kernel sums (bias + q) x products, with a
+    bias of 64 (INT4), 64 / 16 / 4 (INT2) or 1024 (INT8) that cancels only
+    at the end, so about 0.3% of the fp16 outputs round to the neighbouring
+    value (rel-L2 ~2e-5). 1e-4 still sits 10x below the oracle's 1e-3."""
     torch = torch_gpu
     specs = [(4096, 4096, 128), (1024, 4096, 128), (1024, 4096, 128),   # q | k | v
              (14336, 4096, 128), (4096, 14336, 128),                    # mixed K in one launch
@@ -527,7 +537,7 @@ def test_grouped_launch_matches_oracle_and_single_calls(torch_gpu, m):
         cases[i].check(ys[i].cpu().numpy(), x16s[i], f"grouped problem {i} M={m}")
         single = ext().gemv(x, *ext_args(pw)).float()
         diff = (ys[i].float() - single).norm() / single.norm().clamp_min(1e-30)
-        assert diff <= 1e-5, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
+        assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
 
 
 def test_grouped_launch_sixteen_problems_and_python_api(torch_gpu):
@@ -541,7 +551,7 @@ def test_grouped_launch_sixteen_problems_and_python_api(torch_gpu):
     for y, x, pw in zip(ys, xs, pws):
         assert y.shape == (1, 1, pw.shape[0])
         single = gemv(x, pw).float()
-        assert (y.float() - single).norm() <= 1e-5 * single.norm()
+        assert (y.float() - single).norm() <= GROUPED_VS_SINGLE_REL_L2 * single.norm()
     with pytest.raises(RuntimeError, match="1..16 problems"):
         ext().gemv_batched(xs * 2, [p.qweight for p in pws] * 2, [p.scales for p in pws] * 2, [None] * 32, 2,
                            [64] * 32, True, True)
