@@ -557,6 +557,42 @@ def test_grouped_launch_sixteen_problems_and_python_api(torch_gpu):
                            [64] * 32, True, True)
 
 
+@pytest.mark.parametrize("bits,gs,sym,n,k,count", [
+    (4, 128, False, 12000, 4096, 8),   # R = 8 tiles
+    (2, 64, False, 8000, 14336, 6),    # R = 4 tiles, 224 chunks per row (3.5 batches)
+    (8, None, True, 8000, 4096, 10),   # per-channel INT8
+])
+def test_grouped_launch_over_several_rounds(torch_gpu, bits, gs, sym, n, k, count):
+    """M = 1 launches with more block-tiles than the persistent grid holds
+    (2500-3000 block-tiles against at most ~2000 resident blocks), so blocks
+    walk several rounds and cross problem boundaries mid-walk. Every problem
+    against the oracle on a sample of rows that includes each problem's last
+    40 rows, and against its single call."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    gen = torch.Generator(device="cuda").manual_seed(bits * 1000 + count)
+    cfg = QuantConfig(bits, gs, sym, "sequential")
+    pws, cases, xs, x16s = [], [], [], []
+    for i in range(count):
+        pw = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02, cfg)
+        rng = np.random.Generator(np.random.PCG64(i))
+        rows = np.unique(np.concatenate([rng.choice(n - 40, 200, replace=False), np.arange(n - 40, n)]))
+        qw, sc = pw.qweight.cpu().numpy(), pw.scales.cpu().numpy()
+        ze = None if pw.zeros is None else pw.zeros.cpu().numpy()
+        cases.append(OracleCase(pw, qw, sc, ze, rows, deq_ref=False))
+        x16s.append(activations(1, k, seed=90 + i))
+        xs.append(to_gpu(torch, x16s[-1]))
+        pws.append(pw)
+    ys = ext().gemv_batched(xs, [p.qweight for p in pws], [p.scales for p in pws], [p.zeros for p in pws], bits,
+                            [p.config.effective_group_size(k) for p in pws], sym, False)
+    for i, (x, pw) in enumerate(zip(xs, pws)):
+        cases[i].check(ys[i].cpu().numpy(), x16s[i], f"INT{bits} [{n},{k}] x{count} problem {i}")
+        single = ext().gemv(x, *ext_args(pw)).float()
+        diff = (ys[i].float() - single).norm() / single.norm().clamp_min(1e-30)
+        assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
+
+
 def test_launch_event_hook_times_the_kernel(torch_gpu):
     torch = torch_gpu
     from dequant_project_amd import _native
