@@ -1147,6 +1147,38 @@ __device__ __forceinline__ void w16_fragments(const u32x4& w, uint32_t sb, uint3
   for (int f = 0; f < F::CPL / 8; ++f) wf[f] = pack8(dq[4 * f], dq[4 * f + 1], dq[4 * f + 2], dq[4 * f + 3]);
 }
 
+// 4 x 4 transpose over the four 16-lane rows of a wave: on entry register q
+// of lane (row, i) holds element (q, row); on exit register j holds element
+// (row, j) of the same lane position i. Two stages of gfx950 lane swaps:
+// permlane32 swaps rows {2, 3} of one register with rows {0, 1} of another,
+// permlane16 rows {1, 3} of one with rows {0, 2} of another.
+__device__ __forceinline__ void swap_rows32(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  const uint32_t x = r[0], y = r[1];
+  a = x;
+  b = y;
+}
+__device__ __forceinline__ void swap_rows16(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  const uint32_t x = r[0], y = r[1];
+  a = x;
+  b = y;
+}
+__device__ __forceinline__ void transpose_rows4(u32x4 (&v)[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint32_t a0 = v[0][e], a1 = v[1][e], a2 = v[2][e], a3 = v[3][e];
+    swap_rows32(a0, a2);
+    swap_rows32(a1, a3);
+    swap_rows16(a0, a1);
+    swap_rows16(a2, a3);
+    v[0][e] = a0;
+    v[1][e] = a1;
+    v[2][e] = a2;
+    v[3][e] = a3;
+  }
+}
+
 template <int BITS, bool SYM, bool INTER, int MB>
 __global__ void __launch_bounds__(kGemvThreads) gemm_mfma_kernel(const GemmBatch b) {
   using F = Fmt<BITS>;
@@ -1199,12 +1231,30 @@ __global__ void __launch_bounds__(kGemvThreads) gemm_mfma_kernel(const GemmBatch
         const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(
             wbuf, cok ? wrow + static_cast<uint32_t>(c) * 16u : kOutOfRange, 0, 2);
         u32x4 xv[MB][CPL / 8];
+        if constexpr (BITS == 4) {
+          // load q reads piece kb of chunk 4t + q, so the four lanes of a row
+          // read that chunk's 64 contiguous bytes (16 rows x 64 B per load, not
+          // 16 rows x 4 pieces 64 B apart); a 4 x 4 transpose over the lane
+          // rows kb then hands lane (kb, r) the four pieces of its own chunk
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+          for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-          for (int q = 0; q < CPL / 8; ++q)
-            xv[mb][q] = __builtin_amdgcn_raw_buffer_load_b128(
-                xbuf, cok ? xrow[mb] + static_cast<uint32_t>(c) * (CPL * 2u) + 16u * q : kOutOfRange, 0, 0);
+            for (int q = 0; q < 4; ++q) {
+              const int cq = 4 * t + q;
+              xv[mb][q] = __builtin_amdgcn_raw_buffer_load_b128(
+                  xbuf, cq < d.n_chunks ? xrow[mb] + static_cast<uint32_t>(cq) * 64u + 16u * kb : kOutOfRange, 0, 0);
+            }
+          }
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) transpose_rows4(xv[mb]);
+        } else {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int q = 0; q < CPL / 8; ++q)
+              xv[mb][q] = __builtin_amdgcn_raw_buffer_load_b128(
+                  xbuf, cok ? xrow[mb] + static_cast<uint32_t>(c) * (CPL * 2u) + 16u * q : kOutOfRange, 0, 0);
+        }
         h8 wf[NF];
         const bool wide = !SYM && (zb & 0x7FFFu) > 0x6400u;
         if (!SYM && __builtin_amdgcn_ballot_w64(wide) != 0)
