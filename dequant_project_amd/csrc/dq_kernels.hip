@@ -27,22 +27,30 @@
 //     contiguously. A chunk holds 128/BITS codes of one group
 //     (group_size % (128/BITS) == 0). Each batch issues the activations, then
 //     every zero, scale and weight load of its R rows, before any math.
-//   * Unpack to exact fp16 (code - zero) pairs in two VALU ops per pair:
+//   * M = 1 unpacks to biased fp16 codes in one VALU op per pair: under an
+//     exponent field of 25 - p, a code masked into mantissa bit p reads
+//     exactly 2^(10-p) + q (v_and_or_b32; INT8: one v_perm_b32), and per row
+//     and chunk sum (q - z) x = sum (bias + q) x - (sum bias x + z sum x) in
+//     fp32, with the two activation sums shared by the tile's rows. Codes sit
+//     at mantissa bits 4..9 (biases <= 64; INT8: 1024), which keeps the fp32
+//     sums' cancellation far inside the reference's error bound, for any
+//     zero point.
+//   * 2 <= M <= 8 and the small GEMM unpack to exact fp16 (code - zero) pairs
+//     in two VALU ops per pair:
 //       v_and_or_b32  (w & mask) | 0x64006400  -> fp16 (1024 + q * 2^p) in both
 //                     halves (q sits in mantissa bits [p, p+BITS), p <= 8);
 //       v_pk_fma_f16  * 2^-p - (2^(10-p) + z)  -> fp16 (q - z), exact.
-//     (INT8 builds the 0x64qq halves with one v_perm_b32 instead.) Pair i holds
-//     the word's slots (i, i + PER/2); the activations are gathered into the
-//     same pair order, so sequential and interleaved layouts cost the same.
+//     Zero points outside [-1024, 1024] (possible: the packer stores them
+//     unclamped) cannot use that form; such tiles take q exactly and subtract
+//     z * sum(x) in fp32 instead (uniform branch, rare).
+//   * Pair i holds the word's slots (i, i + PER/2); the activations are
+//     gathered into the same pair order, so sequential and interleaved
+//     layouts cost the same.
 //   * v_dot2_f32_f16 (or, for INT2, the diagonal of v_mfma_f32_4x4x4_16b_f16)
-//     multiplies (q - z) pairs with activation pairs and accumulates in fp32;
-//     per chunk, acc * scale is added in fp32 -- the reference's arithmetic
-//     (fp32 accumulation of exact (q - z) * x products, factorized scale), so
-//     the reference's elementwise fp32 error bound holds. 2 <= M <= 8 runs
-//     the same arithmetic on the matrix cores (gemv_quad_kernel).
-//   * Zero points outside [-1024, 1024] (possible: the packer stores them
-//     unclamped) cannot use the exact fp16 form; such chunks take q exactly and
-//     subtract z * sum(x) in fp32 instead (uniform branch, rare).
+//     multiplies code pairs with activation pairs and accumulates in fp32;
+//     per chunk, acc * scale is added in fp32 -- the reference's factorized
+//     scale, within its elementwise fp32 error bound. 2 <= M <= 8 runs the
+//     exact form on the matrix cores (gemv_quad_kernel).
 //   * Rows are finished with a DPP wave64 reduction (row_shr 1/2/4/8,
 //     row_bcast 15/31) instead of an LDS tree; fp16 (RNE) stores.
 //
