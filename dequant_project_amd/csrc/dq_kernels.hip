@@ -690,7 +690,76 @@ __device__ __forceinline__ void finish_tile_rms(const KernelProblem& d, const Ti
   }
 }
 
-template <int BITS, bool SYM, bool INTER, int R, bool MF, int PRO>
+// Workgroup barrier for LDS traffic only. Its release / acquire fences are
+// scoped to LDS, so a wave waits for its own LDS writes (lgkmcnt) but not for
+// its global loads in flight; __syncthreads() fences every address space,
+// i.e. waits for all of the wave's outstanding global loads before the
+// barrier (checked in the generated code: vmcnt(0) there, only lgkmcnt(0)
+// here).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Activations of one M = 1 batch staged in LDS for the whole block (XL):
+// the 64 chunk columns of the batch, one padded 16-byte-aligned slot per
+// chunk (a lane's reads then spread over the banks). Used when every tile of
+// the launch is one wave wide (wk = 1), so the block's four waves walk the
+// same chunk columns in step: one coalesced load per block instead of one per
+// wave (INT2 carries as many activation bytes per lane as weight bytes).
+template <int BITS>
+struct XStage {
+  static constexpr int kChunkBytes = Fmt<BITS>::CPL * 2;
+  static constexpr int kPieces = kChunkBytes / 16;
+  static constexpr int kStride = kChunkBytes + 16;
+  static constexpr int kBufBytes = 64 * kStride;
+  static constexpr int kPerThread = (64 * kPieces + kGemvThreads - 1) / kGemvThreads;
+};
+
+template <int BITS>
+__device__ __forceinline__ void xstage_issue(const KernelProblem& d, const TilePos& tb,
+                                             u32x4 (&st)[XStage<BITS>::kPerThread]) {
+  using XS = XStage<BITS>;
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(d.K) * 2u);
+#pragma unroll
+  for (int i = 0; i < XS::kPerThread; ++i) {
+    const int e = static_cast<int>(threadIdx.x) + kGemvThreads * i;
+    const int cc = e / XS::kPieces, pc = e % XS::kPieces;
+    const int c = tb.cb + cc;
+    st[i] = __builtin_amdgcn_raw_buffer_load_b128(
+        xbuf, e < 64 * XS::kPieces && c < tb.ce ? static_cast<uint32_t>(c) * XS::kChunkBytes + 16u * pc : kOutOfRange,
+        0, 0);
+  }
+}
+
+template <int BITS>
+__device__ __forceinline__ void xstage_write(unsigned char* buf, const u32x4 (&st)[XStage<BITS>::kPerThread]) {
+  using XS = XStage<BITS>;
+#pragma unroll
+  for (int i = 0; i < XS::kPerThread; ++i) {
+    const int e = static_cast<int>(threadIdx.x) + kGemvThreads * i;
+    if (e < 64 * XS::kPieces)
+      *reinterpret_cast<u32x4*>(buf + (e / XS::kPieces) * XS::kStride + 16 * (e % XS::kPieces)) = st[i];
+  }
+}
+
+template <int BITS, bool INTER>
+__device__ __forceinline__ void xstage_read(const unsigned char* buf, int lane, h2 (&xr)[4][Fmt<BITS>::PAIRS]) {
+  using F = Fmt<BITS>;
+  using XS = XStage<BITS>;
+  uint32_t xd[F::CPL / 2];
+#pragma unroll
+  for (int k = 0; k < XS::kPieces; ++k) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(buf + lane * XS::kStride + 16 * k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xd[4 * k + e] = v[e];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xr[j]);
+}
+
+template <int BITS, bool SYM, bool INTER, int R, bool MF, int PRO, bool XL>
 __global__ void __launch_bounds__(kGemvThreads)
 gemv_m1_kernel(const KernelBatch b) {
   using F = Fmt<BITS>;
@@ -698,10 +767,12 @@ gemv_m1_kernel(const KernelBatch b) {
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   __shared__ float part[2][kWavesPerBlock][PW];
+  __shared__ __align__(16) unsigned char xl[XL ? 2 * XStage<BITS>::kBufBytes : 16];
   ClassMagics<BITS> cm;
   cm.init();
   const int total = b.bt_start[b.count];
   int phase = 0;
+  int parity = 0;  // XL: staging buffer of the next batch, across tiles
   int p = 0;
   for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
     const TilePos t = locate(b, bt, wave, R, p);
@@ -710,7 +781,9 @@ gemv_m1_kernel(const KernelBatch b) {
 #pragma unroll
     for (int r = 0; r < R; ++r) yacc[r] = 0.f;
     float ssq = 0.f;  // RMSNorm prologue: this wave's sum(x^2)
-    if (t.active) {
+    // XL: every wave of the block, active or not, walks the batches (they
+    // stage the activations together and meet at each batch's barrier)
+    if (XL || t.active) {
       for (int cbase = t.cb; cbase < t.ce; cbase += 64) {
         TilePos tb = t;
         tb.cb = cbase;
@@ -720,23 +793,37 @@ gemv_m1_kernel(const KernelBatch b) {
         // whole tile had arrived
         h2 xr[1][4][F::PAIRS];
         XRaw<BITS, PRO> raw;
-        if constexpr (PRO == kProNone)
-          load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
-        else
-          issue_x_pro<BITS, PRO>(d, tb, lane, 0, 1, raw);
         TileLoads<BITS, R, 1> L;
-        issue_tile_m1<BITS, SYM, R>(d, tb, lane, L);
-        // keep every load of the batch ahead of its math: left alone, the
-        // scheduler sinks the weight loads into the math to save registers,
-        // leaving one or two rows in flight and the latency exposed per row
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (PRO != kProNone) x_pairs_pro<BITS, INTER, PRO>(raw, xr[0], ssq);
-        float acc[R];
+        if constexpr (XL) {
+          unsigned char* buf = xl + parity * XStage<BITS>::kBufBytes;
+          parity ^= 1;
+          u32x4 st[XStage<BITS>::kPerThread];
+          xstage_issue<BITS>(d, tb, st);
+          if (t.active) issue_tile_m1<BITS, SYM, R>(d, tb, lane, L);
+          __builtin_amdgcn_sched_barrier(0);
+          xstage_write<BITS>(buf, st);
+          lds_barrier();  // the weights stay in flight
+          xstage_read<BITS, INTER>(buf, lane, xr[0]);
+        } else {
+          if constexpr (PRO == kProNone)
+            load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
+          else
+            issue_x_pro<BITS, PRO>(d, tb, lane, 0, 1, raw);
+          issue_tile_m1<BITS, SYM, R>(d, tb, lane, L);
+          // keep every load of the batch ahead of its math: left alone, the
+          // scheduler sinks the weight loads into the math to save registers,
+          // leaving one or two rows in flight and the latency exposed per row
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (PRO != kProNone) x_pairs_pro<BITS, INTER, PRO>(raw, xr[0], ssq);
+        }
+        if (t.active) {
+          float acc[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.f;
-        tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr[0], cm, lane, acc);
+          for (int r = 0; r < R; ++r) acc[r] = 0.f;
+          tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr[0], cm, lane, acc);
 #pragma unroll
-        for (int r = 0; r < R; ++r) yacc[r] += acc[r];
+          for (int r = 0; r < R; ++r) yacc[r] += acc[r];
+        }
       }
     }
     if constexpr (PRO == kProRmsNorm)
@@ -1537,6 +1624,16 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
   return bts;
 }
 
+// Activations staged per block in LDS (gemv_m1_kernel<..., XL = true>) for
+// INT2, whose lanes load as many activation bytes as weight bytes, in
+// launches where every tile is one wave wide, a tile holds at least two
+// batches (K >= 8192) and the persistent grid walks at least kXlRounds rounds
+// of block-tiles (the variant holds three waves per SIMD, not four).
+// Measured: C5 stack (K = 8192 / 28672 MLP) +7%; K = 4096 tiles of one batch
+// no change; a 2.3-round decode launch -4% (hence the rounds floor).
+constexpr bool m1_stages_x(int bits) { return bits == 2; }
+constexpr int kXlRounds = 4;
+
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
   int wks[kMaxBatch];
@@ -1545,7 +1642,14 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
   const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
   kb.eps = eps;
   if (bts == 0) return hipSuccess;
-  constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO>;
+  if constexpr (m1_stages_x(BITS) && PRO == kProNone) {
+    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, true>;
+    bool stage = true;
+    for (int i = 0; i < count; ++i) stage = stage && wks[i] == 1 && kb.p[i].n_chunks >= 2 * 64;
+    const int grid = resident_blocks<kernel>();
+    if (stage && bts >= kXlRounds * grid) return launch_kernel(kernel, grid, kb, stream);
+  }
+  constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, false>;
   return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
 }
 

@@ -561,13 +561,18 @@ def test_grouped_launch_sixteen_problems_and_python_api(torch_gpu):
     (4, 128, False, 12000, 4096, 8),   # R = 8 tiles
     (2, 64, False, 8000, 14336, 6),    # R = 4 tiles, 224 chunks per row (3.5 batches)
     (8, None, True, 8000, 4096, 10),   # per-channel INT8
+    (2, 64, False, 8192, 8192, 16),    # INT2 with activations staged per block in LDS:
+                                       # 4096 block-tiles of two batches, >= 4 rounds
 ])
 def test_grouped_launch_over_several_rounds(torch_gpu, bits, gs, sym, n, k, count):
     """M = 1 launches with more block-tiles than the persistent grid holds
-    (2500-3000 block-tiles against at most ~2000 resident blocks), so blocks
-    walk several rounds and cross problem boundaries mid-walk. Every problem
-    against the oracle on a sample of rows that includes each problem's last
-    40 rows, and against its single call."""
+    (2500-4096 block-tiles against at most ~2000 resident blocks), so blocks
+    walk several rounds and cross problem boundaries mid-walk; the last case
+    is large enough (every tile one wave wide, two batches per tile, at least
+    four rounds of the 768-block grid) for the INT2 kernel that stages the
+    activations per block in LDS. Every problem against the oracle on a sample
+    of rows that includes each problem's last 40 rows, and against its single
+    call (which, 64 times smaller, runs the unstaged kernel)."""
     torch = torch_gpu
     from dequant_project_amd.packer import QuantConfig, quantize_tensor
 
