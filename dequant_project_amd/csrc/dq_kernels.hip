@@ -1655,11 +1655,13 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
 
 // Geometry of the quad kernel (2 <= M <= 8): tiles of 4 * kQuadsPerTile rows,
 // MG = 1 batch-row group of 4 for M <= 4, else 2; wk as for the M = 1 kernel
-// (tiles of 16 rows), the same for every problem of the launch (the smallest
+// (tiles of 8 rows), the same for every problem of the launch (the smallest
 // of the problems' choices; capped at 2 for INT2 with MG = 2, whose staging
 // buffers would otherwise take 132 KiB of LDS), each wave's share rounded up
-// to whole steps of 16 chunks.
-constexpr int kQuadsPerTile = 4;
+// to whole steps of 16 chunks. Two quads per tile measured best on the C4
+// stack (M = 2 / 4 / 8: +2 / +4 / +16% over four, whose accumulators and
+// operands held M = 8 to two waves per SIMD; one quad lost 4-17%).
+constexpr int kQuadsPerTile = 2;
 
 int quad_waves_per_tile(const GemvOperand* ops, int count, int bits, int mg) {
   int wks[kMaxBatch];

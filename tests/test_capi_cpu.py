@@ -222,13 +222,13 @@ def test_gemv_plan_geometry():
     assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 3)  # 172 columns of 64 codes, 43 per wave
     assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 2)  # INT8 wants 8192 waves
     # 2 <= M <= 8: gemv_quad_kernel (kind 1) for every format and group size;
-    # 16-row tiles, wk by the M = 1 rule for 16-row tiles.
-    assert plan([(4096, 4096)], m=4) == ([2], 16, 1)
-    assert plan([(14336, 4096)] * 2, m=8) == ([2, 2], 16, 1)
-    assert plan([(11008, 4096)], m=4, bits=8, gs=None) == ([4], 16, 1)
-    assert plan([(4096, 11008)], m=4, bits=2, gs=64) == ([4], 16, 1)
-    assert plan([(4096, 4096)], m=2, gs=64) == ([2], 16, 1)
-    assert plan([(14336, 4096)] * 16, m=2) == ([1] * 16, 16, 1)
+    # 8-row tiles (two quads), wk by the M = 1 rule for 8-row tiles.
+    assert plan([(4096, 4096)], m=4) == ([2], 8, 1)
+    assert plan([(14336, 4096)] * 2, m=8) == ([2, 2], 8, 1)
+    assert plan([(11008, 4096)], m=4, bits=8, gs=None) == ([4], 8, 1)
+    assert plan([(4096, 11008)], m=4, bits=2, gs=64) == ([4], 8, 1)
+    assert plan([(4096, 4096)], m=2, gs=64) == ([2], 8, 1)
+    assert plan([(14336, 4096)] * 16, m=2) == ([1] * 16, 8, 1)
     arr = (_native.DqGemvProblem * 1)()
     arr[0].N, arr[0].K, arr[0].group_size = 8, 100, 100
     wk, rows, kind = (ctypes.c_int * 1)(), ctypes.c_int(), ctypes.c_int()
