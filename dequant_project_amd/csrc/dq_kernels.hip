@@ -141,35 +141,6 @@ __device__ __forceinline__ void magic_pairs(uint32_t w, uint32_t magic, uint32_t
   }
 }
 
-// Per (row, chunk) constants turning magic pairs of class c into (q - z):
-// (1024 + q 2^p) * 2^-p + off[c] with off[c] = -(2^(10-p) + z), computed in
-// fp16 straight from the stored zero (exact: |2^(10-p) + z| <= 2048). Zero
-// points outside [-1024, 1024] (or not finite) cannot use the exact form; then
-// off[c] = -2^(10-p) yields q alone and the caller subtracts z * sum(x).
-template <int BITS, bool SYM>
-__device__ __forceinline__ bool class_offsets(uint16_t zbits, h2* off) {
-  using F = Fmt<BITS>;
-  bool exact = true;
-  _Float16 z;
-  if constexpr (SYM) {
-    z = static_cast<_Float16>(static_cast<float>(F::BIAS));
-  } else {
-    exact = (zbits & 0x7FFFu) <= 0x6400u;  // |z| <= 1024 on the fp16 bit pattern
-    z = exact ? __builtin_bit_cast(_Float16, zbits) : static_cast<_Float16>(0.0f);
-  }
-  const h2 zz = splat(z);
-#pragma unroll
-  for (int c = 0; c < F::NCLS; c += 2) {
-    const _Float16 b0 = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c))));
-    const _Float16 b1 = c + 1 < F::NCLS ? static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(c + 1))))
-                                        : b0;
-    const h2 both = -(h2{b0, b1} + zz);  // one v_pk_add_f16 for two classes
-    off[c] = splat(both.x);
-    if (c + 1 < F::NCLS) off[c + 1] = splat(both.y);
-  }
-  return exact;
-}
-
 // ------------------------------------------------------------ wave reduction
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_move(float v) {
