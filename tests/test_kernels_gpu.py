@@ -285,6 +285,34 @@ def check_gemm_small(torch, pw, qw, sc, ze, ms, label):
         assert rl2 <= REL_L2_TOL, f"{label} M={m}: rel-L2 {rl2:.3e}"
 
 
+def test_random_formats_and_shapes_sweep(torch_gpu):
+    """A seeded sweep over the operand space the C ABI accepts: 36 cases of
+    random bits, layout, symmetry, group size (a multiple of one 16-byte
+    chunk's codes, or per-channel), ragged N up to 2500, K up to ~6000 and
+    M in 1..8, each GEMV against the oracle's two tolerances; every third
+    case also runs the small GEMM at an M in 9..64 against the dequantized
+    product. Shapes no fixed test names (odd N, K of a few chunks, groups
+    that straddle a batch of 64 chunks) land here."""
+    torch = torch_gpu
+    rng = np.random.Generator(np.random.PCG64(2026))
+    for case in range(36):
+        bits = int(rng.choice([2, 4, 8]))
+        cpl = 128 // bits
+        layout = str(rng.choice(["sequential", "interleaved"]))
+        sym = bool(rng.integers(2))
+        groups = [g for g in (16, 32, 64, 128, 256) if g % cpl == 0] + [None]
+        gs = groups[int(rng.integers(len(groups)))]
+        unit = cpl if gs is None else gs
+        k = unit * int(rng.integers(1, max(2, 6144 // unit)))
+        n = int(rng.integers(1, 2501))
+        m = int(rng.choice([1, 1, 2, 3, 5, 8]))
+        label = f"sweep {case}: INT{bits} g{gs} {'sym' if sym else 'asym'} {layout} [{n},{k}]"
+        pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(n, k, seed=3000 + case), bits, gs, sym, layout)
+        check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=4000 + case)], label)
+        if case % 3 == 0:
+            check_gemm_small(torch, pw, qw, sc, ze, (int(rng.integers(9, 65)),), label)
+
+
 GEMM_SMALL_CASES = [
     ((4, 128, False, "sequential"), 1000, 4096),
     ((4, 32, True, "interleaved"), 256, 96),       # 3 chunks: a partial iteration of 4
