@@ -1602,7 +1602,8 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
 // batches (K >= 8192) and the persistent grid walks at least kXlRounds rounds
 // of block-tiles (the variant holds three waves per SIMD, not four).
 // Measured: C5 stack (K = 8192 / 28672 MLP) +7%; K = 4096 tiles of one batch
-// no change; a 2.3-round decode launch -4% (hence the rounds floor).
+// no change; a 2.3-round decode launch -4% (hence the rounds floor); the
+// same staging on every multi-round INT4 launch: INT4 stack -2.6%.
 constexpr bool m1_stages_x(int bits) { return bits == 2; }
 constexpr int kXlRounds = 4;
 
