@@ -13,7 +13,8 @@
 //                         (2 <= M <= 8)
 //   dequantize_kernel  <- dequantize_kernel<BITS,SYM,INTER>        :113-140
 //   gemm_mfma_kernel   (new: the M > 8 product of quant_linear.py:131-132,
-//                      dequantize + F.linear, in one pass for M <= 64)
+//                      dequantize + F.linear, in one pass for M <= 64;
+//                      gemm_shared_x_kernel: its large M <= 16 launches)
 //   unpack_kernel      (new: exposes the unpack step for bit-exact checks)
 //   add_one_kernel     <- kernels/smoke.cu:9-13
 //
@@ -1376,6 +1377,145 @@ __global__ void __launch_bounds__(kGemvThreads) gemm_mfma_kernel(const GemmBatch
   }
 }
 
+// Small GEMM for M <= 16 with the activations shared across tiles. A block
+// of 16 waves holds 4 tiles of 16 rows x 4 K-shares (wave w: tile w / 4,
+// K-share w % 4), the same split along K as gemm_mfma_kernel at wk = 4. Each
+// iteration (4 chunks per lane, lane (kb, r) as there) the 256 threads of a
+// K-share stage its 16 batch rows x 4 chunks of activations in LDS, one
+// 16-byte piece per thread (a wave's load covers 4 rows x 256 contiguous
+// bytes), and all 16 waves meet at an LDS-only barrier (the weight loads stay
+// in flight); each wave reads its A fragments from LDS. gemm_mfma_kernel
+// loads every wave's activations itself: four times the activation loads,
+// which counters showed the texture-address units spending most of their
+// time on. The four K-share partials of a tile meet in LDS.
+constexpr int kSxWaves = 16;
+constexpr int kSxThreads = 64 * kSxWaves;
+constexpr int kSxMinBlocks = 192;  // three quarters of the MI355X's 256 CUs
+
+template <int BITS>
+struct SxStage {
+  static constexpr int kChunkBytes = Fmt<BITS>::CPL * 2;
+  static constexpr int kPieces = kChunkBytes / 16;             // 16-byte pieces per chunk
+  static constexpr int kRowBytes = 4 * kChunkBytes + 16;       // a batch row's 4 chunks, padded
+  static constexpr int kShareBytes = 16 * kRowBytes;           // 16 batch rows
+  static constexpr int kBufBytes = 4 * kShareBytes;            // 4 K-shares
+  static constexpr int kPieceCount = 16 * 4 * kPieces;         // pieces of one share per iteration
+  static constexpr int kPerThread = (kPieceCount + 255) / 256; // per thread of the share's 256
+};
+
+template <int BITS, bool SYM, bool INTER>
+__global__ void __launch_bounds__(kSxThreads) gemm_shared_x_kernel(const GemmBatch b) {
+  using F = Fmt<BITS>;
+  using SX = SxStage<BITS>;
+  constexpr int CPL = F::CPL, NF = CPL / 8;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, kb = lane >> 4;
+  const int slot = wave >> 2, kw = wave & 3;
+  const int tk = slot * 64 + lane;  // this thread's index among the 256 of its K-share
+  __shared__ __align__(16) unsigned char xs_lds[2 * SX::kBufBytes];
+  __shared__ float part[kSxWaves][4][64];
+  const uint32_t magic = magic_vgpr();
+  const int total = b.bt_start[b.count];
+  int parity = 0;
+  int p = 0;
+  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
+    while (p + 1 < b.count && bt >= b.bt_start[p + 1]) ++p;
+    const GemmProblem& d = b.p[p];
+    const int tile = (bt - b.bt_start[p]) * 4 + slot;
+    const bool active = tile < d.tiles;
+    const int row0 = tile * 16;
+    const int ib = kw * d.per_wave;
+    const int ie = min(d.n_iters, ib + d.per_wave);
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+    const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
+    const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+    const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row);
+    const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row);
+    const uint32_t kbytes = static_cast<uint32_t>(d.K) * 2u;
+    const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(b.M) * kbytes);
+    const uint32_t n = static_cast<uint32_t>(min(row0 + r, d.N - 1));  // past N: re-read, never stored
+    const uint32_t wrow = n * row_bytes, mrow = n * meta_row;
+    // every wave, active or not, runs every iteration of the block's problem
+    // (the K-shares stage together and meet at each iteration's barrier)
+    for (int t = 0; t < d.per_wave; ++t) {
+      unsigned char* buf = xs_lds + parity * SX::kBufBytes;
+      parity ^= 1;
+      const bool iok = ib + t < ie;
+      // this K-share's activations of the iteration: piece e of 16 rows x 4 chunks
+      u32x4 st[SX::kPerThread];
+#pragma unroll
+      for (int i = 0; i < SX::kPerThread; ++i) {
+        const int e = tk + 256 * i;
+        const int piece = e % SX::kPieces, cc = (e / SX::kPieces) % 4, m = e / (SX::kPieces * 4);
+        const int c = 4 * (ib + t) + cc;
+        const bool ok = e < SX::kPieceCount && iok && m < b.M && c < d.n_chunks;
+        st[i] = __builtin_amdgcn_raw_buffer_load_b128(
+            xbuf, ok ? static_cast<uint32_t>(m) * kbytes + static_cast<uint32_t>(c) * SX::kChunkBytes + 16u * piece
+                     : kOutOfRange,
+            0, 0);
+      }
+      const int c = 4 * (ib + t) + kb;
+      const bool cok = active && iok && c < d.n_chunks;
+      const uint32_t g = d.n_groups == 1 ? 0u
+                         : (d.cpg_shift >= 0 ? static_cast<uint32_t>(c) >> d.cpg_shift
+                                             : static_cast<uint32_t>(c) / static_cast<uint32_t>(d.cpg));
+      const uint32_t zb = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(zbuf, cok ? mrow + g * 2u : kOutOfRange, 0, 0);
+      const uint32_t sb = __builtin_amdgcn_raw_buffer_load_b16(sbuf, cok ? mrow + g * 2u : kOutOfRange, 0, 0);
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(
+          wbuf, cok ? wrow + static_cast<uint32_t>(c) * 16u : kOutOfRange, 0, 2);
+      __builtin_amdgcn_sched_barrier(0);  // every global load of the iteration is in flight before the staging waits
+#pragma unroll
+      for (int i = 0; i < SX::kPerThread; ++i) {
+        const int e = tk + 256 * i;
+        const int piece = e % SX::kPieces, cc = (e / SX::kPieces) % 4, m = e / (SX::kPieces * 4);
+        if (e < SX::kPieceCount)
+          *reinterpret_cast<u32x4*>(buf + kw * SX::kShareBytes + m * SX::kRowBytes + cc * SX::kChunkBytes +
+                                     16 * piece) = st[i];
+      }
+      lds_barrier();
+      h8 wf[NF];
+      const bool wide = !SYM && (zb & 0x7FFFu) > 0x6400u;
+      if (!SYM && __builtin_amdgcn_ballot_w64(wide) != 0)
+        w16_fragments<BITS, SYM, true>(w, sb, zb, magic, wf);
+      else
+        w16_fragments<BITS, SYM, false>(w, sb, zb, magic, wf);
+      // chunk kb of the iteration, batch row r, in the weights' pair order
+      uint32_t xd[CPL / 2];
+      const unsigned char* xrow = buf + kw * SX::kShareBytes + r * SX::kRowBytes + kb * SX::kChunkBytes;
+#pragma unroll
+      for (int q = 0; q < CPL / 8; ++q) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(xrow + 16 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xd[4 * q + e] = v[e];
+      }
+      h2 xp[CPL / 2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp + j * F::PAIRS);
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pack8(xp[4 * f], xp[4 * f + 1], xp[4 * f + 2], xp[4 * f + 3]),
+                                                     wf[f], acc, 0, 0, 0);
+    }
+    // lane (kb, r) holds y[4 kb + i][row0 + r]; the 4 K-shares of a tile meet in LDS
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[wave][i][lane] = acc[i];
+    __syncthreads();
+    if (active && kw == 0) {
+      const int ncol = row0 + r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = part[wave][i][lane] + part[wave + 1][i][lane] + part[wave + 2][i][lane] +
+                        part[wave + 3][i][lane];
+        const int m = 4 * kb + i;
+        if (m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.N + ncol] = f32_to_f16_rn(v);
+      }
+    }
+    __syncthreads();  // the partials are read before the next tile writes them
+  }
+}
+
 // ---------------------------------------------------------------- dequantize
 constexpr int kElemThreads = 256;
 
@@ -1528,12 +1668,12 @@ int log2_exact(int64_t v) {  // log2 of a power of two, else -1
 thread_local hipEvent_t t_start_event = nullptr, t_stop_event = nullptr;
 
 template <typename Kernel, typename Batch>
-hipError_t launch_kernel(Kernel kernel, int blocks, const Batch& kb, hipStream_t stream) {
+hipError_t launch_kernel(Kernel kernel, int blocks, const Batch& kb, hipStream_t stream, int threads = kGemvThreads) {
   if (t_start_event && t_stop_event) {
-    hipExtLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), 0, stream, t_start_event, t_stop_event, 0, kb);
+    hipExtLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), 0, stream, t_start_event, t_stop_event, 0, kb);
     t_start_event = t_stop_event = nullptr;
   } else {
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kGemvThreads), 0, stream, kb);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(threads), 0, stream, kb);
   }
   return hipGetLastError();
 }
@@ -1542,14 +1682,14 @@ hipError_t launch_kernel(Kernel kernel, int blocks, const Batch& kb, hipStream_t
 // per instance: the cache is keyed by the kernel itself (a template argument),
 // because every instance of one kernel template has the same function type.
 // The engine targets a single device model, the MI355X.
-template <auto Kernel>
+template <auto Kernel, int THREADS = kGemvThreads>
 int resident_blocks() {
   static int cached = 0;
   if (cached == 0) {
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, kGemvThreads, 0) != hipSuccess || cus <= 0 ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, THREADS, 0) != hipSuccess || cus <= 0 ||
         per_cu <= 0) {
       (void)hipGetLastError();
       return 512;
@@ -1728,6 +1868,31 @@ hipError_t launch_gemm_mb(const GemvOperand* ops, int count, int64_t M, hipStrea
   }
   gb.bt_start[count] = bts;
   if (bts == 0) return hipSuccess;
+  if constexpr (MB == 1 && BITS != 2) {
+    // M <= 16 with every tile split 4 ways along K and enough tiles for
+    // kSxMinBlocks 16-wave blocks: the variant that shares each K-share's
+    // activations across 4 tiles. Measured at M = 16 on the Llama-3-8B shapes:
+    // gate/up_proj (224 blocks) 29.5 -> 20.8 us; down_proj and q|o_proj
+    // (64 blocks: three quarters of the CUs idle) 2x slower, so they stay on
+    // the 4-wave kernel. INT2, whose lanes carry 128 bytes of activations per
+    // chunk, stays there too.
+    bool four = true;
+    int sbts = 0;
+    for (int i = 0; i < count; ++i) {
+      four = four && wks[i] == 4;
+      sbts += (gb.p[i].tiles + 3) / 4;
+    }
+    if (four && sbts >= kSxMinBlocks) {
+      sbts = 0;
+      for (int i = 0; i < count; ++i) {
+        gb.bt_start[i] = sbts;
+        sbts += (gb.p[i].tiles + 3) / 4;
+      }
+      gb.bt_start[count] = sbts;
+      constexpr auto kernel = gemm_shared_x_kernel<BITS, SYM, INTER>;
+      return launch_kernel(kernel, std::min(sbts, resident_blocks<kernel, kSxThreads>()), gb, stream, kSxThreads);
+    }
+  }
   constexpr auto kernel = gemm_mfma_kernel<BITS, SYM, INTER, MB>;
   return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), gb, stream);
 }

@@ -285,6 +285,38 @@ def check_gemm_small(torch, pw, qw, sc, ze, ms, label):
         assert rl2 <= REL_L2_TOL, f"{label} M={m}: rel-L2 {rl2:.3e}"
 
 
+@pytest.mark.parametrize("fmt", [(4, 128, False, "sequential"), (4, 64, True, "interleaved"),
+                                 (8, None, True, "sequential")])
+def test_gemm_small_shared_activation_kernel(torch_gpu, fmt):
+    """gemm_small at M <= 16 on a gate_proj shape (14336 x 4096: 896 tiles of
+    16 rows, split 4 ways along K, 224 blocks of 16 waves), which runs the
+    variant that shares each K-share's activations across 4 tiles, against
+    the dequantized product on a sample of rows including the last tile."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    n, k = 14336, 4096
+    gen = torch.Generator(device="cuda").manual_seed(77)
+    pw = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02,
+                         QuantConfig(*fmt))
+    rows = np.unique(np.concatenate([np.random.Generator(np.random.PCG64(5)).choice(n - 16, 300, replace=False),
+                                     np.arange(n - 16, n)]))
+    qw, sc = pw.qweight[rows].cpu().numpy(), pw.scales[rows].cpu().numpy()
+    ze = None if pw.zeros is None else pw.zeros[rows].cpu().numpy()
+    cfg = P.Config(*fmt)
+    w16 = P.dequantize(qw, sc, ze, cfg, (len(rows), k)).astype(np.float64)
+    for m in (3, 9, 16):
+        x16 = activations(m, k, seed=200 + m)
+        y = ext().gemm_small(to_gpu(torch, x16), *ext_args(pw)).cpu().numpy()[:, rows]
+        ref = x16.astype(np.float64) @ w16.T
+        absref = np.abs(x16.astype(np.float64)) @ np.abs(w16).T
+        ok, worst = P.gemv_criterion(y, ref, absref)
+        rl2 = P.rel_l2(y, ref)
+        print(f"shared-activation gemm {fmt} M={m}: worst={worst:.3f}x tol rel_l2={rl2:.2e}", flush=True)
+        assert ok, f"{fmt} M={m}: elementwise criterion violated, worst {worst:.3f}x tol"
+        assert rl2 <= REL_L2_TOL, f"{fmt} M={m}: rel-L2 {rl2:.3e}"
+
+
 def test_random_formats_and_shapes_sweep(torch_gpu):
     """A seeded sweep over the operand space the C ABI accepts: 36 cases of
     random bits, layout, symmetry, group size (a multiple of one 16-byte
