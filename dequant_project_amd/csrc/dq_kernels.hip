@@ -14,7 +14,7 @@
 //   dequantize_kernel  <- dequantize_kernel<BITS,SYM,INTER>        :113-140
 //   gemm_mfma_kernel   (new: the M > 8 product of quant_linear.py:131-132,
 //                      dequantize + F.linear, in one pass for M <= 64;
-//                      gemm_shared_x_kernel: its large M <= 16 launches)
+//                      gemm_shared_x_kernel: its large M <= 32 launches)
 //   unpack_kernel      (new: exposes the unpack step for bit-exact checks)
 //   add_one_kernel     <- kernels/smoke.cu:9-13
 //
@@ -1388,33 +1388,35 @@ __global__ void __launch_bounds__(kGemvThreads) gemm_mfma_kernel(const GemmBatch
 // loads every wave's activations itself: four times the activation loads,
 // which counters showed the texture-address units spending most of their
 // time on. The four K-share partials of a tile meet in LDS.
-constexpr int kSxWaves = 16;
-constexpr int kSxThreads = 64 * kSxWaves;
 constexpr int kSxMinBlocks = 192;  // three quarters of the MI355X's 256 CUs
 
-template <int BITS>
+// TPB tiles x 4 K-shares per block; MB activation tiles of 16 rows.
+template <int BITS, int MB, int TPB>
 struct SxStage {
+  static constexpr int kWaves = 4 * TPB;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kShareThreads = 64 * TPB;                 // threads of one K-share
   static constexpr int kChunkBytes = Fmt<BITS>::CPL * 2;
-  static constexpr int kPieces = kChunkBytes / 16;             // 16-byte pieces per chunk
-  static constexpr int kRowBytes = 4 * kChunkBytes + 16;       // a batch row's 4 chunks, padded
-  static constexpr int kShareBytes = 16 * kRowBytes;           // 16 batch rows
-  static constexpr int kBufBytes = 4 * kShareBytes;            // 4 K-shares
-  static constexpr int kPieceCount = 16 * 4 * kPieces;         // pieces of one share per iteration
-  static constexpr int kPerThread = (kPieceCount + 255) / 256; // per thread of the share's 256
+  static constexpr int kPieces = kChunkBytes / 16;               // 16-byte pieces per chunk
+  static constexpr int kRowBytes = 4 * kChunkBytes + 16;         // a batch row's 4 chunks, padded
+  static constexpr int kShareBytes = 16 * MB * kRowBytes;        // 16 MB batch rows
+  static constexpr int kBufBytes = 4 * kShareBytes;              // 4 K-shares
+  static constexpr int kPieceCount = 16 * MB * 4 * kPieces;      // pieces of one share per iteration
+  static constexpr int kPerThread = (kPieceCount + kShareThreads - 1) / kShareThreads;
 };
 
-template <int BITS, bool SYM, bool INTER>
-__global__ void __launch_bounds__(kSxThreads) gemm_shared_x_kernel(const GemmBatch b) {
+template <int BITS, bool SYM, bool INTER, int MB, int TPB>
+__global__ void __launch_bounds__(256 * TPB) gemm_shared_x_kernel(const GemmBatch b) {
   using F = Fmt<BITS>;
-  using SX = SxStage<BITS>;
+  using SX = SxStage<BITS, MB, TPB>;
   constexpr int CPL = F::CPL, NF = CPL / 8;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, kb = lane >> 4;
   const int slot = wave >> 2, kw = wave & 3;
-  const int tk = slot * 64 + lane;  // this thread's index among the 256 of its K-share
+  const int tk = slot * 64 + lane;  // this thread's index among the threads of its K-share
   __shared__ __align__(16) unsigned char xs_lds[2 * SX::kBufBytes];
-  __shared__ float part[kSxWaves][4][64];
+  __shared__ float part[SX::kWaves][4 * MB][64];
   const uint32_t magic = magic_vgpr();
   const int total = b.bt_start[b.count];
   int parity = 0;
@@ -1422,12 +1424,14 @@ __global__ void __launch_bounds__(kSxThreads) gemm_shared_x_kernel(const GemmBat
   for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
     while (p + 1 < b.count && bt >= b.bt_start[p + 1]) ++p;
     const GemmProblem& d = b.p[p];
-    const int tile = (bt - b.bt_start[p]) * 4 + slot;
+    const int tile = (bt - b.bt_start[p]) * TPB + slot;
     const bool active = tile < d.tiles;
     const int row0 = tile * 16;
     const int ib = kw * d.per_wave;
     const int ie = min(d.n_iters, ib + d.per_wave);
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    f4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
     const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
     const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
     const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
@@ -1443,11 +1447,11 @@ __global__ void __launch_bounds__(kSxThreads) gemm_shared_x_kernel(const GemmBat
       unsigned char* buf = xs_lds + parity * SX::kBufBytes;
       parity ^= 1;
       const bool iok = ib + t < ie;
-      // this K-share's activations of the iteration: piece e of 16 rows x 4 chunks
+      // this K-share's activations of the iteration: piece e of 16 MB rows x 4 chunks
       u32x4 st[SX::kPerThread];
 #pragma unroll
       for (int i = 0; i < SX::kPerThread; ++i) {
-        const int e = tk + 256 * i;
+        const int e = tk + SX::kShareThreads * i;
         const int piece = e % SX::kPieces, cc = (e / SX::kPieces) % 4, m = e / (SX::kPieces * 4);
         const int c = 4 * (ib + t) + cc;
         const bool ok = e < SX::kPieceCount && iok && m < b.M && c < d.n_chunks;
@@ -1468,7 +1472,7 @@ __global__ void __launch_bounds__(kSxThreads) gemm_shared_x_kernel(const GemmBat
       __builtin_amdgcn_sched_barrier(0);  // every global load of the iteration is in flight before the staging waits
 #pragma unroll
       for (int i = 0; i < SX::kPerThread; ++i) {
-        const int e = tk + 256 * i;
+        const int e = tk + SX::kShareThreads * i;
         const int piece = e % SX::kPieces, cc = (e / SX::kPieces) % 4, m = e / (SX::kPieces * 4);
         if (e < SX::kPieceCount)
           *reinterpret_cast<u32x4*>(buf + kw * SX::kShareBytes + m * SX::kRowBytes + cc * SX::kChunkBytes +
@@ -1481,36 +1485,44 @@ __global__ void __launch_bounds__(kSxThreads) gemm_shared_x_kernel(const GemmBat
         w16_fragments<BITS, SYM, true>(w, sb, zb, magic, wf);
       else
         w16_fragments<BITS, SYM, false>(w, sb, zb, magic, wf);
-      // chunk kb of the iteration, batch row r, in the weights' pair order
-      uint32_t xd[CPL / 2];
-      const unsigned char* xrow = buf + kw * SX::kShareBytes + r * SX::kRowBytes + kb * SX::kChunkBytes;
 #pragma unroll
-      for (int q = 0; q < CPL / 8; ++q) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(xrow + 16 * q);
+      for (int mb = 0; mb < MB; ++mb) {
+        // chunk kb of the iteration, batch row 16 mb + r, in the weights' pair order
+        uint32_t xd[CPL / 2];
+        const unsigned char* xrow =
+            buf + kw * SX::kShareBytes + (16 * mb + r) * SX::kRowBytes + kb * SX::kChunkBytes;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xd[4 * q + e] = v[e];
+        for (int q = 0; q < CPL / 8; ++q) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(xrow + 16 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xd[4 * q + e] = v[e];
+        }
+        h2 xp[CPL / 2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp + j * F::PAIRS);
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              pack8(xp[4 * f], xp[4 * f + 1], xp[4 * f + 2], xp[4 * f + 3]), wf[f], acc[mb], 0, 0, 0);
       }
-      h2 xp[CPL / 2];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp + j * F::PAIRS);
-#pragma unroll
-      for (int f = 0; f < NF; ++f)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pack8(xp[4 * f], xp[4 * f + 1], xp[4 * f + 2], xp[4 * f + 3]),
-                                                     wf[f], acc, 0, 0, 0);
     }
-    // lane (kb, r) holds y[4 kb + i][row0 + r]; the 4 K-shares of a tile meet in LDS
+    // lane (kb, r) holds y[16 mb + 4 kb + i][row0 + r]; the 4 K-shares of a tile meet in LDS
 #pragma unroll
-    for (int i = 0; i < 4; ++i) part[wave][i][lane] = acc[i];
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[wave][4 * mb + i][lane] = acc[mb][i];
     __syncthreads();
     if (active && kw == 0) {
       const int ncol = row0 + r;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = part[wave][i][lane] + part[wave + 1][i][lane] + part[wave + 2][i][lane] +
-                        part[wave + 3][i][lane];
-        const int m = 4 * kb + i;
-        if (m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.N + ncol] = f32_to_f16_rn(v);
-      }
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = part[wave][4 * mb + i][lane] + part[wave + 1][4 * mb + i][lane] +
+                          part[wave + 2][4 * mb + i][lane] + part[wave + 3][4 * mb + i][lane];
+          const int m = 16 * mb + 4 * kb + i;
+          if (m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.N + ncol] = f32_to_f16_rn(v);
+        }
     }
     __syncthreads();  // the partials are read before the next tile writes them
   }
@@ -1868,29 +1880,34 @@ hipError_t launch_gemm_mb(const GemvOperand* ops, int count, int64_t M, hipStrea
   }
   gb.bt_start[count] = bts;
   if (bts == 0) return hipSuccess;
-  if constexpr (MB == 1 && BITS != 2) {
-    // M <= 16 with every tile split 4 ways along K and enough tiles for
-    // kSxMinBlocks 16-wave blocks: the variant that shares each K-share's
-    // activations across 4 tiles. Measured at M = 16 on the Llama-3-8B shapes:
-    // gate/up_proj (224 blocks) 29.5 -> 20.8 us; down_proj and q|o_proj
+  if constexpr (MB <= 2 && BITS != 2) {
+    // Every tile split 4 ways along K and enough tiles for kSxMinBlocks
+    // blocks: the variant that shares each K-share's activations across the
+    // block's tiles (4 tiles at M <= 16, 2 at M <= 32, where the registers
+    // allow two waves per SIMD). Measured on the Llama-3-8B shapes: gate/up_proj
+    // 29.5 -> 20.8 us at M = 16 (224 blocks), 44.0 -> 31.7 us at M = 32 (448
+    // blocks); at M = 16 down_proj and q|o_proj
     // (64 blocks: three quarters of the CUs idle) 2x slower, so they stay on
     // the 4-wave kernel. INT2, whose lanes carry 128 bytes of activations per
     // chunk, stays there too.
+    constexpr int TPB = MB == 1 ? 4 : 2;
     bool four = true;
     int sbts = 0;
     for (int i = 0; i < count; ++i) {
       four = four && wks[i] == 4;
-      sbts += (gb.p[i].tiles + 3) / 4;
+      sbts += (gb.p[i].tiles + TPB - 1) / TPB;
     }
     if (four && sbts >= kSxMinBlocks) {
       sbts = 0;
       for (int i = 0; i < count; ++i) {
         gb.bt_start[i] = sbts;
-        sbts += (gb.p[i].tiles + 3) / 4;
+        sbts += (gb.p[i].tiles + TPB - 1) / TPB;
       }
       gb.bt_start[count] = sbts;
-      constexpr auto kernel = gemm_shared_x_kernel<BITS, SYM, INTER>;
-      return launch_kernel(kernel, std::min(sbts, resident_blocks<kernel, kSxThreads>()), gb, stream, kSxThreads);
+      using SX = SxStage<BITS, MB, TPB>;
+      constexpr auto kernel = gemm_shared_x_kernel<BITS, SYM, INTER, MB, TPB>;
+      return launch_kernel(kernel, std::min(sbts, resident_blocks<kernel, SX::kThreads>()), gb, stream,
+                           SX::kThreads);
     }
   }
   constexpr auto kernel = gemm_mfma_kernel<BITS, SYM, INTER, MB>;

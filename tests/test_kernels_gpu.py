@@ -288,9 +288,10 @@ def check_gemm_small(torch, pw, qw, sc, ze, ms, label):
 @pytest.mark.parametrize("fmt", [(4, 128, False, "sequential"), (4, 64, True, "interleaved"),
                                  (8, None, True, "sequential")])
 def test_gemm_small_shared_activation_kernel(torch_gpu, fmt):
-    """gemm_small at M <= 16 on a gate_proj shape (14336 x 4096: 896 tiles of
-    16 rows, split 4 ways along K, 224 blocks of 16 waves), which runs the
-    variant that shares each K-share's activations across 4 tiles, against
+    """gemm_small at M <= 32 on a gate_proj shape (14336 x 4096: 896 tiles of
+    16 rows, split 4 ways along K), which runs the variant that shares each
+    K-share's activations across the block's tiles (M <= 16: 4 tiles, 224
+    blocks of 16 waves; M <= 32: 2 tiles, 448 blocks of 8 waves), against
     the dequantized product on a sample of rows including the last tile."""
     torch = torch_gpu
     from dequant_project_amd.packer import QuantConfig, quantize_tensor
@@ -305,7 +306,7 @@ def test_gemm_small_shared_activation_kernel(torch_gpu, fmt):
     ze = None if pw.zeros is None else pw.zeros[rows].cpu().numpy()
     cfg = P.Config(*fmt)
     w16 = P.dequantize(qw, sc, ze, cfg, (len(rows), k)).astype(np.float64)
-    for m in (3, 9, 16):
+    for m in (3, 9, 16, 24, 32):
         x16 = activations(m, k, seed=200 + m)
         y = ext().gemm_small(to_gpu(torch, x16), *ext_args(pw)).cpu().numpy()[:, rows]
         ref = x16.astype(np.float64) @ w16.T
