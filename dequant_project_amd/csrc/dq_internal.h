@@ -60,9 +60,6 @@ constexpr int kMaxGemmM = 64;
 hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
                              bool interleaved, hipStream_t stream);
 
-// Waves per 16-row tile along K for each problem of a small-GEMM launch.
-void plan_gemm_batch(const GemvOperand* ops, int count, int bits, int* wk);
-
 struct DequantProblem {
   const uint32_t* qweight;
   const uint16_t* scales;

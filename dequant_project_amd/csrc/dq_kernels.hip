@@ -1246,14 +1246,14 @@ __device__ __forceinline__ void transpose_rows4(u32x4 (&v)[4]) {
   }
 }
 
-template <int BITS, bool SYM, bool INTER, int MB>
-__global__ void __launch_bounds__(kGemvThreads) gemm_mfma_kernel(const GemmBatch b) {
+template <int BITS, bool SYM, bool INTER, int MB, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) gemm_mfma_kernel(const GemmBatch b) {
   using F = Fmt<BITS>;
   constexpr int CPL = F::CPL, NF = CPL / 8;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, kb = lane >> 4;
-  __shared__ float part[2][kWavesPerBlock][MB * 4][64];
+  __shared__ float part[2][WAVES][MB * 4][64];
   const uint32_t magic = magic_vgpr();
   const int total = b.bt_start[b.count];
   int phase = 0;
@@ -1264,7 +1264,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemm_mfma_kernel(const GemmBatch
     const int wk = 1 << d.lwk;
     const int slot = wave >> d.lwk;
     const int kw = wave & (wk - 1);
-    const int tile = ((bt - b.bt_start[p]) << (2 - d.lwk)) + slot;
+    const int tile = (bt - b.bt_start[p]) * (WAVES >> d.lwk) + slot;  // WAVES / wk tiles per block-tile
     const bool active = tile < d.tiles;
     const int row0 = tile * 16;
     const int ib = kw * d.per_wave;
@@ -1824,10 +1824,10 @@ hipError_t launch_gemv_quad(const GemvOperand* ops, int count, int64_t M, hipStr
 // leaving each wave at least 4 iterations of 4 chunks.
 constexpr int64_t kGemmWaves = 4096;
 
-int gemm_waves_per_tile(const GemvOperand* ops, int count, int bits, int* wk) {
+int gemm_waves_per_tile(const GemvOperand* ops, int count, int bits, int max_wk, int* wk) {
   const int cpl = 128 / bits;
   int w = 1;
-  for (; w < 4; w *= 2) {
+  for (; w < max_wk; w *= 2) {
     int64_t waves = 0;
     for (int i = 0; i < count; ++i) {
       const int64_t iters = (ops[i].K / cpl + 3) / 4;
@@ -1846,72 +1846,85 @@ int gemm_waves_per_tile(const GemvOperand* ops, int count, int bits, int* wk) {
   return w;
 }
 
+// Waves per block of gemm_mfma_kernel, and so the largest split along K: 8
+// for M <= 32, 4 above. Measured on the Llama-3-8B shapes against 4-wave
+// blocks: at M = 16 q|k|v|o_proj -8% and down_proj -11% (one tile per block
+// split 8 ways: the same 256 blocks, half the iterations per wave), at
+// M = 32 the small shapes -4%; at M = 64 the large ones +2% (so 4 stay).
+// 16-wave blocks put two tiles in a block and halved the blocks of a q_proj
+// launch: +45%.
+template <int BITS, int MB>
+constexpr int gemm_block_waves() {
+  return MB <= 2 ? 8 : 4;
+}
+
 template <int BITS, bool SYM, bool INTER, int MB>
 hipError_t launch_gemm_mb(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
   constexpr int CPL = 128 / BITS;
+  constexpr int WAVES = gemm_block_waves<BITS, MB>();
+  auto fill = [&](const int* wks, int waves_per_block, GemmBatch& gb) {
+    gb = GemmBatch{};
+    gb.count = count;
+    gb.M = static_cast<int>(M);
+    int bts = 0;
+    for (int i = 0; i < count; ++i) {
+      const GemvOperand& o = ops[i];
+      GemmProblem& k = gb.p[i];
+      k.qweight = o.qweight;
+      k.scales = o.scales;
+      k.zeros = o.zeros;
+      k.x = o.x;
+      k.y = o.y;
+      k.N = static_cast<int>(o.N);
+      k.K = static_cast<int>(o.K);
+      k.n_groups = static_cast<int>(o.K / o.group_size);
+      k.cpg = static_cast<int>(o.group_size / CPL);
+      k.cpg_shift = log2_exact(k.cpg);
+      k.n_chunks = static_cast<int>(o.K / CPL);
+      k.n_iters = (k.n_chunks + 3) / 4;
+      const int wk = wks[i];
+      k.lwk = log2_exact(wk);
+      k.per_wave = (k.n_iters + wk - 1) / wk;
+      k.tiles = static_cast<int>((o.N + 15) / 16);
+      const int tiles_per_bt = waves_per_block / wk;
+      gb.bt_start[i] = bts;
+      bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
+    }
+    gb.bt_start[count] = bts;
+    return bts;
+  };
+  GemmBatch gb;
   int wks[kMaxBatch];
-  gemm_waves_per_tile(ops, count, BITS, wks);
-  GemmBatch gb{};
-  gb.count = count;
-  gb.M = static_cast<int>(M);
-  int bts = 0;
-  for (int i = 0; i < count; ++i) {
-    const GemvOperand& o = ops[i];
-    GemmProblem& k = gb.p[i];
-    k.qweight = o.qweight;
-    k.scales = o.scales;
-    k.zeros = o.zeros;
-    k.x = o.x;
-    k.y = o.y;
-    k.N = static_cast<int>(o.N);
-    k.K = static_cast<int>(o.K);
-    k.n_groups = static_cast<int>(o.K / o.group_size);
-    k.cpg = static_cast<int>(o.group_size / CPL);
-    k.cpg_shift = log2_exact(k.cpg);
-    k.n_chunks = static_cast<int>(o.K / CPL);
-    k.n_iters = (k.n_chunks + 3) / 4;
-    const int wk = wks[i];
-    k.lwk = log2_exact(wk);
-    k.per_wave = (k.n_iters + wk - 1) / wk;
-    k.tiles = static_cast<int>((o.N + 15) / 16);
-    const int tiles_per_bt = kWavesPerBlock / wk;
-    gb.bt_start[i] = bts;
-    bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
-  }
-  gb.bt_start[count] = bts;
-  if (bts == 0) return hipSuccess;
   if constexpr (MB <= 2 && BITS != 2) {
     // Every tile split 4 ways along K and enough tiles for kSxMinBlocks
     // blocks: the variant that shares each K-share's activations across the
     // block's tiles (4 tiles at M <= 16, 2 at M <= 32, where the registers
     // allow two waves per SIMD). Measured on the Llama-3-8B shapes: gate/up_proj
     // 29.5 -> 20.8 us at M = 16 (224 blocks), 44.0 -> 31.7 us at M = 32 (448
-    // blocks); at M = 16 down_proj and q|o_proj
-    // (64 blocks: three quarters of the CUs idle) 2x slower, so they stay on
-    // the 4-wave kernel. INT2, whose lanes carry 128 bytes of activations per
-    // chunk, stays there too.
+    // blocks); at M = 16 down_proj and q|o_proj (64 blocks: three quarters of
+    // the CUs idle) ran 2x slower in it. INT2, whose lanes carry 128 bytes of
+    // activations per chunk, does not take it.
     constexpr int TPB = MB == 1 ? 4 : 2;
+    gemm_waves_per_tile(ops, count, BITS, 4, wks);
     bool four = true;
     int sbts = 0;
     for (int i = 0; i < count; ++i) {
       four = four && wks[i] == 4;
-      sbts += (gb.p[i].tiles + TPB - 1) / TPB;
+      sbts += static_cast<int>(((ops[i].N + 15) / 16 + TPB - 1) / TPB);
     }
     if (four && sbts >= kSxMinBlocks) {
-      sbts = 0;
-      for (int i = 0; i < count; ++i) {
-        gb.bt_start[i] = sbts;
-        sbts += (gb.p[i].tiles + TPB - 1) / TPB;
-      }
-      gb.bt_start[count] = sbts;
+      fill(wks, 4 * TPB, gb);
       using SX = SxStage<BITS, MB, TPB>;
       constexpr auto kernel = gemm_shared_x_kernel<BITS, SYM, INTER, MB, TPB>;
       return launch_kernel(kernel, std::min(sbts, resident_blocks<kernel, SX::kThreads>()), gb, stream,
                            SX::kThreads);
     }
   }
-  constexpr auto kernel = gemm_mfma_kernel<BITS, SYM, INTER, MB>;
-  return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), gb, stream);
+  gemm_waves_per_tile(ops, count, BITS, WAVES, wks);
+  const int bts = fill(wks, WAVES, gb);
+  if (bts == 0) return hipSuccess;
+  constexpr auto kernel = gemm_mfma_kernel<BITS, SYM, INTER, MB, WAVES>;
+  return launch_kernel(kernel, std::min(bts, resident_blocks<kernel, 64 * WAVES>()), gb, stream, 64 * WAVES);
 }
 
 template <int BITS, bool SYM, bool INTER>
@@ -2042,7 +2055,6 @@ hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int b
 #undef DQ_CALL_GEMM
 }
 
-void plan_gemm_batch(const GemvOperand* ops, int count, int bits, int* wk) { gemm_waves_per_tile(ops, count, bits, wk); }
 
 hipError_t launch_dequantize(const DequantProblem& p, hipStream_t stream) {
 #define DQ_CALL_DEQ(B, S, I) launch_dequantize_t<B, S, I>(p, stream)
