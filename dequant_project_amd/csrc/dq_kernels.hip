@@ -47,8 +47,8 @@
 //   * Pair i holds the word's slots (i, i + PER/2); the activations are
 //     gathered into the same pair order, so sequential and interleaved
 //     layouts cost the same.
-//   * v_dot2_f32_f16 (or, for INT2, the diagonal of v_mfma_f32_4x4x4_16b_f16)
-//     multiplies code pairs with activation pairs and accumulates in fp32;
+//   * v_dot2_f32_f16 (a diagonal-of-v_mfma_f32_4x4x4_16b_f16 form exists and
+//     measured slower) multiplies code pairs with activation pairs and accumulates in fp32;
 //     per chunk, acc * scale is added in fp32 -- the reference's factorized
 //     scale, within its elementwise fp32 error bound. 2 <= M <= 8 runs the
 //     exact form on the matrix cores (gemv_quad_kernel).
@@ -1631,11 +1631,13 @@ int64_t elementwise_blocks(int64_t items) {
 // so a problem's result is deterministic for a given launch but may differ in
 // the last bits between a grouped launch and a single one.
 // M = 1 dot products on the matrix cores (gemv_m1_kernel<..., MF = true)?
-// Measured on the Llama-3-8B stack shapes (8-row tiles): INT2 g64 48.3% of
-// peak with MFMA vs 46.1% on the VALU (its 16 codes per word make v_dot2 the
-// largest VALU item); INT4 and INT8 within noise or slower, so they stay on
-// the VALU.
-constexpr bool m1_uses_mfma(int bits) { return bits == 2; }
+// With exact (q - z) codes INT2 g64 measured 48.3% of peak with MFMA vs 46.1%
+// on the VALU (v_dot2 was then its largest VALU item). With the biased codes
+// the VALU form needs no accumulator registers and measured better: C4 INT2
+// stack 4270 -> 4345 GB/s, C5 stack 5457 -> 5558 GB/s; INT4 and INT8 were
+// within noise or slower with MFMA in both forms. So no format uses it; the
+// MF form stays as the measured alternative.
+constexpr bool m1_uses_mfma(int) { return false; }
 constexpr int64_t kWideTiles = 6144;
 constexpr int64_t kProWideTiles = 2048;  // prologue launches: see launch_gemv_prologue_t
 constexpr int64_t kMinColumns = 40;

@@ -211,9 +211,9 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
  *                      rows_per_tile, false> (M = 1; VALU dot products), or
  *   *kernel_kind == 3: gemv_m1_kernel<bits, symmetric, interleaved,
  *                      rows_per_tile, true> (M = 1; dot products on the
- *                      matrix cores; used for bits == 2; large launches of
- *                      one-wave tiles with K >= 8192 take its variant that
- *                      stages the activations per block in LDS).
+ *                      matrix cores; not chosen by the current geometry).
+ * Large INT2 launches of one-wave tiles with K >= 8192 take the M = 1
+ * kernel's variant that stages the activations per block in LDS.
  * The geometry is chosen per launch, so a problem's result is deterministic
  * for a given launch but may differ in the last bits between a grouped launch
  * and a single one. waves_per_tile must hold `count` ints. */
