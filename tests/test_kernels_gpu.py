@@ -622,6 +622,7 @@ def test_grouped_launch_sixteen_problems_and_python_api(torch_gpu):
     (4, 128, False, 12000, 4096, 8),   # R = 8 tiles
     (2, 64, False, 8000, 14336, 6),    # R = 4 tiles, 224 chunks per row (3.5 batches)
     (8, None, True, 8000, 4096, 10),   # per-channel INT8
+    (2, 64, False, 4093, 4096, 16),    # INT2 rows under 8192 codes, last 8-row tile partial
     (2, 64, False, 8165, 8192, 16),    # INT2 with activations staged per block in LDS:
                                        # 4096 block-tiles of two batches, >= 4 rounds; each
                                        # problem's last block-tile holds one 5-row tile and
