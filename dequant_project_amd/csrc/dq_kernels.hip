@@ -167,6 +167,43 @@ __device__ __forceinline__ void wave_sum_lane63(float* v) {
   for (int i = 0; i < N; ++i) v[i] += dpp_move<0x143, 0xc>(v[i]);  // row_bcast:31 into rows 2, 3
 }
 
+// Sums over the 64 lanes of a wave for R = 4 or 8 values, halving the values
+// per lane at each exchange. The gfx950 permlane32 swap of (a, b) leaves
+// a = rows {0, 1} of a then of b and b = rows {2, 3} of a then of b;
+// permlane16 leaves a = rows (a0, b0, a2, b2) and b = (a1, b1, a3, b3).
+// Swapping value i with value i + R/2 and adding gives, in lanes 0-31, value
+// i summed over both halves of the wave and, in lanes 32-63, value i + R/2;
+// the permlane16 swap of i with i + R/4 then leaves row g holding value
+// i + g R/4 summed over its four lane-sets, and four in-row DPP steps finish.
+// Lane 16 g + 15 ends with the totals of values g R/4 + i in v[i],
+// i < R/4: 5R/4 + 4 instructions where wave_sum_lane63 takes 6R.
+template <int R>
+__device__ __forceinline__ void wave_sum_rows(float (&v)[R]) {
+  static_assert(R == 4 || R == 8, "rows per tile");
+#pragma unroll
+  for (int i = 0; i < R / 2; ++i) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v[i]),
+                                                    __builtin_bit_cast(uint32_t, v[i + R / 2]), false, false);
+    const uint32_t a = p[0], b = p[1];  // element by element: see swap_sum16
+    v[i] = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  }
+#pragma unroll
+  for (int i = 0; i < R / 4; ++i) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v[i]),
+                                                    __builtin_bit_cast(uint32_t, v[i + R / 4]), false, false);
+    const uint32_t a = p[0], b = p[1];
+    v[i] = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  }
+#pragma unroll
+  for (int i = 0; i < R / 4; ++i) v[i] += dpp_move<0x111, 0xf>(v[i]);  // row_shr:1
+#pragma unroll
+  for (int i = 0; i < R / 4; ++i) v[i] += dpp_move<0x112, 0xf>(v[i]);  // row_shr:2
+#pragma unroll
+  for (int i = 0; i < R / 4; ++i) v[i] += dpp_move<0x114, 0xf>(v[i]);  // row_shr:4
+#pragma unroll
+  for (int i = 0; i < R / 4; ++i) v[i] += dpp_move<0x118, 0xf>(v[i]);  // row_shr:8: lane 16g+15
+}
+
 // ---------------------------------------------------------------------- gemv
 constexpr int kGemvThreads = 256;  // 4 waves
 constexpr int kWavesPerBlock = kGemvThreads / 64;
@@ -430,16 +467,36 @@ __device__ __forceinline__ void store_row_block(uint16_t* y, int row0, int N, co
   }
 }
 
+// Rows r .. r + Q - 1 of y from one lane (Q = 1 or 2): one 4-byte store when
+// both rows exist and y + r is aligned for it.
+template <int Q>
+__device__ __forceinline__ void store_rows(uint16_t* y, int r, int N, const float* v) {
+  uint16_t* dst = y + r;
+  if constexpr (Q == 2) {
+    if (r + 2 <= N && (reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
+      *reinterpret_cast<uint32_t*>(dst) =
+          static_cast<uint32_t>(f32_to_f16_rn(v[0])) | (static_cast<uint32_t>(f32_to_f16_rn(v[1])) << 16);
+      return;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < Q; ++i)
+    if (r + i < N) dst[i] = f32_to_f16_rn(v[i]);
+}
+
 template <int R>
 __device__ __forceinline__ void finish_tile(const KernelProblem& d, const TilePos& t, int wave, int lane,
                                             float (&yacc)[R], float (*part)[R]) {
-  wave_sum_lane63<R>(yacc);
+  constexpr int Q = R / 4;  // rows per holder lane 16 g + 15, from row g Q of the tile
+  wave_sum_rows<R>(yacc);
+  const bool holder = (lane & 15) == 15;
+  const int g = lane >> 4;
   if (t.wk == 1) {
-    if (t.active && lane == 63) store_row_block<R>(d.y, t.row0, d.N, yacc);
+    if (t.active && holder) store_rows<Q>(d.y, t.row0 + g * Q, d.N, yacc);
   } else {
-    if (lane == 63) {
+    if (holder) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) part[wave][r] = yacc[r];
+      for (int i = 0; i < Q; ++i) part[wave][g * Q + i] = yacc[i];
     }
     __syncthreads();  // all 4 waves of the block run the same block-tile sequence
     if (t.active && t.kw == 0 && lane < R) {
