@@ -259,6 +259,7 @@ struct KernelBatch {
   int count;
   int M;
   float eps;  // RMSNorm prologue epsilon
+  int run;    // gemv_m1_kernel<..., kXmKeep>: block-tiles per run of the walk
 };
 
 // Where block-tile `bt` of the launch sits, as seen by one wave. All fields
@@ -665,13 +666,13 @@ __device__ __forceinline__ float biased_dot_m1(const u32x4& w, const h2 (&xr)[4]
   }
 }
 
-// One batch of a tile: acc[r] = scale_r * (sum (bias + q) x - (C + z_r S)).
-template <int BITS, bool SYM, bool INTER, int R, bool MF>
-__device__ __forceinline__ void tile_math_m1(const TileLoads<BITS, R, 1>& L, const h2 (&xr)[4][Fmt<BITS>::PAIRS],
-                                             const ClassMagics<BITS>& cm, int lane, float (&acc)[R]) {
+// One batch of a tile, given the batch's bias sums S and C:
+// acc[r] = scale_r * (sum (bias + q) x - (C + z_r S)).
+template <int BITS, bool SYM, int R, bool MF>
+__device__ __forceinline__ void tile_math_m1_sums(const TileLoads<BITS, R, 1>& L,
+                                                  const h2 (&xr)[4][Fmt<BITS>::PAIRS], float S, float C,
+                                                  const ClassMagics<BITS>& cm, int lane, float (&acc)[R]) {
   using F = Fmt<BITS>;
-  float S, C;
-  bias_sums<BITS>(xr, S, C);
   if constexpr (SYM) C = __builtin_fmaf(static_cast<float>(F::BIAS), S, C);  // z = 2^(b-1) for every row
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -679,6 +680,14 @@ __device__ __forceinline__ void tile_math_m1(const TileLoads<BITS, R, 1>& L, con
     const float v = biased_dot_m1<BITS, MF>(L.w[0][r], xr, cm, lane) - corr;
     acc[r] = __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(L.s[0][r])), v, acc[r]);
   }
+}
+
+template <int BITS, bool SYM, bool INTER, int R, bool MF>
+__device__ __forceinline__ void tile_math_m1(const TileLoads<BITS, R, 1>& L, const h2 (&xr)[4][Fmt<BITS>::PAIRS],
+                                             const ClassMagics<BITS>& cm, int lane, float (&acc)[R]) {
+  float S, C;
+  bias_sums<BITS>(xr, S, C);
+  tile_math_m1_sums<BITS, SYM, R, MF>(L, xr, S, C, cm, lane, acc);
 }
 
 // finish_tile for the RMSNorm prologue: the R dot products and the wave's
@@ -731,7 +740,7 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Activations of one M = 1 batch staged in LDS for the whole block (XL):
+// Activations of one M = 1 batch staged in LDS for the whole block (kXmStage):
 // the 64 chunk columns of the batch, one padded 16-byte-aligned slot per
 // chunk (a lane's reads then spread over the banks). Used when every tile of
 // the launch is one wave wide (wk = 1), so the block's four waves walk the
@@ -788,10 +797,24 @@ __device__ __forceinline__ void xstage_read(const unsigned char* buf, int lane, 
   for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xr[j]);
 }
 
-template <int BITS, bool SYM, bool INTER, int R, bool MF, int PRO, bool XL>
+// Where an M = 1 launch's activations come from (gemv_m1_kernel's XM):
+//   kXmLoad   every wave loads each batch's activations;
+//   kXmStage  the block stages each batch's activations once in LDS (XStage);
+//   kXmKeep   tiles of one batch, each block walking a contiguous range of
+//             block-tiles: a wave keeps the activation pairs of its last tile
+//             in its own LDS slot (8 KiB for INT2) and their bias sums in
+//             registers, and loads x again only when a tile reads other
+//             columns or another x (the q | k | v and gate | up problems of a
+//             layer share x, so most tiles of a long range reuse them).
+enum : int { kXmLoad = 0, kXmStage = 1, kXmKeep = 2 };
+
+template <int BITS, bool SYM, bool INTER, int R, bool MF, int PRO, int XM>
 __global__ void __launch_bounds__(kGemvThreads)
 gemv_m1_kernel(const KernelBatch b) {
   using F = Fmt<BITS>;
+  constexpr bool XL = XM == kXmStage;
+  constexpr bool KEEP = XM == kXmKeep;
+  static_assert(!KEEP || (PRO == kProNone && !MF), "kept activations: plain VALU launches");
   constexpr int PW = PRO == kProRmsNorm ? R + 1 : R;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
@@ -803,7 +826,23 @@ gemv_m1_kernel(const KernelBatch b) {
   int phase = 0;
   int parity = 0;  // XL: staging buffer of the next batch, across tiles
   int p = 0;
-  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
+  // block-tiles in runs of `run` consecutive ones, the runs strided over the
+  // grid: run = 1 is the plain grid-stride walk. KEEP walks runs of b.run
+  // (2 or 3), so a wave's consecutive tiles are neighbours while the
+  // block-tiles in flight across the chip stay one compact span of the launch
+  // (a contiguous share per block spread them over the whole launch and cost
+  // 7.7% on the C4 INT2 stack before any reuse)
+  const int run = KEEP ? b.run : 1;
+  // KEEP: the pairs (in this wave's LDS slot) and bias sums of the last
+  // activations this wave loaded, and the x and chunk columns they came from
+  __shared__ u32x4 xkeep[KEEP ? kWavesPerBlock * F::PAIRS * 64 : 1];
+  float Sk = 0.f, Ck = 0.f;
+  bool have = false;
+  const void* kx = nullptr;
+  int kcb = 0, kce = 0;
+  int bt = static_cast<int>(blockIdx.x) * run;  // run r, element j: (r * gridDim.x + blockIdx.x) * run + j
+  int in_run = 0;
+  while (bt < total) {
     const TilePos t = locate(b, bt, wave, R, p);
     const KernelProblem& d = b.p[t.p];
     float yacc[R];
@@ -833,6 +872,38 @@ gemv_m1_kernel(const KernelBatch b) {
           xstage_write<BITS>(buf, st);
           lds_barrier();  // the weights stay in flight
           xstage_read<BITS, INTER>(buf, lane, xr[0]);
+        } else if constexpr (KEEP) {
+          // the tile's one batch (tb == t); a fresh load keeps the order of
+          // the path below (activations first), the pairs replace the kept ones
+          u32x4* kept = xkeep + wave * F::PAIRS * 64;  // piece q of lane l at q * 64 + l
+          if (!have || d.x != kx || tb.cb != kcb || tb.ce != kce) {
+            load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
+            issue_tile_m1<BITS, SYM, R>(d, tb, lane, L);
+            __builtin_amdgcn_sched_barrier(0);
+            bias_sums<BITS>(xr[0], Sk, Ck);
+#pragma unroll
+            for (int q = 0; q < F::PAIRS; ++q) {
+              u32x4 v;
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                v[e] = __builtin_bit_cast(uint32_t, xr[0][(4 * q + e) / F::PAIRS][(4 * q + e) % F::PAIRS]);
+              kept[q * 64 + lane] = v;
+            }
+            have = true;
+            kx = d.x;
+            kcb = tb.cb;
+            kce = tb.ce;
+          } else {
+            // one wave's own LDS slot: its reads follow its earlier writes in order
+#pragma unroll
+            for (int q = 0; q < F::PAIRS; ++q) {
+              const u32x4 v = kept[q * 64 + lane];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) xr[0][(4 * q + e) / F::PAIRS][(4 * q + e) % F::PAIRS] = as_h2(v[e]);
+            }
+            issue_tile_m1<BITS, SYM, R>(d, tb, lane, L);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         } else {
           if constexpr (PRO == kProNone)
             load_x_columns<BITS, INTER, 1>(d, tb, lane, 0, xr);
@@ -849,7 +920,10 @@ gemv_m1_kernel(const KernelBatch b) {
           float acc[R];
 #pragma unroll
           for (int r = 0; r < R; ++r) acc[r] = 0.f;
-          tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr[0], cm, lane, acc);
+          if constexpr (KEEP)
+            tile_math_m1_sums<BITS, SYM, R, MF>(L, xr[0], Sk, Ck, cm, lane, acc);
+          else
+            tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr[0], cm, lane, acc);
 #pragma unroll
           for (int r = 0; r < R; ++r) yacc[r] += acc[r];
         }
@@ -860,6 +934,16 @@ gemv_m1_kernel(const KernelBatch b) {
     else
       finish_tile<R>(d, t, wave, lane, yacc, part[phase]);
     if (t.wk > 1) phase ^= 1;
+    if constexpr (KEEP) {
+      if (++in_run == run) {
+        in_run = 0;
+        bt += (static_cast<int>(gridDim.x) - 1) * run + 1;
+      } else {
+        ++bt;
+      }
+    } else {
+      bt += gridDim.x;
+    }
   }
 }
 
@@ -1807,7 +1891,7 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
   return bts;
 }
 
-// Activations staged per block in LDS (gemv_m1_kernel<..., XL = true>) for
+// Activations staged per block in LDS (gemv_m1_kernel<..., kXmStage>) for
 // INT2, whose lanes load as many activation bytes as weight bytes, in
 // launches where every tile is one wave wide, a tile holds at least two
 // batches (K >= 8192) and the persistent grid walks at least kXlRounds rounds
@@ -1818,6 +1902,25 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
 constexpr bool m1_stages_x(int bits) { return bits == 2; }
 constexpr int kXlRounds = 4;
 
+// Activations kept across tiles (gemv_m1_kernel<..., kXmKeep>) for INT2
+// launches of 8-row, one-batch tiles (K <= 4096, one wave per tile): the grid
+// walks runs of `run` consecutive block-tiles, the longest run of 3 or 2 that
+// still gives every resident block at least one run (shorter launches keep
+// the plain walk). A wave's tiles within a run mostly read the same x. (The
+// variant's 33 KiB of LDS per block allow four waves per SIMD: the 8-row
+// tiles' register count allows no more, the 4-row tiles' six.) Measured on
+// the C4 INT2 stack: with the activation loads removed altogether (a timing
+// copy) 12.6% faster; runs of 3 on its 3488-block-tile launches (1.1 rounds
+// of runs) 31.8 -> 29.1 us, on its 2752-block-tile launches (0.9 rounds)
+// unchanged; runs of 4 over the whole stack +0.9%, one contiguous share per
+// block +0.4% (the walk alone -7.7%).
+constexpr bool m1_keeps_x(int bits) { return bits == 2; }
+int keep_run(int bts, int grid) {
+  for (int run = 3; run >= 2; --run)
+    if (bts >= run * grid) return run;
+  return 0;
+}
+
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
   int wks[kMaxBatch];
@@ -1827,13 +1930,21 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
   kb.eps = eps;
   if (bts == 0) return hipSuccess;
   if constexpr (m1_stages_x(BITS) && PRO == kProNone) {
-    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, true>;
+    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, kXmStage>;
     bool stage = true;
     for (int i = 0; i < count; ++i) stage = stage && wks[i] == 1 && kb.p[i].n_chunks >= 2 * 64;
     const int grid = resident_blocks<kernel>();
     if (stage && bts >= kXlRounds * grid) return launch_kernel(kernel, grid, kb, stream);
   }
-  constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, false>;
+  if constexpr (m1_keeps_x(BITS) && PRO == kProNone && !m1_uses_mfma(BITS) && R == 8) {
+    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, false, PRO, kXmKeep>;
+    bool keep = true;
+    for (int i = 0; i < count; ++i) keep = keep && wks[i] == 1 && kb.p[i].n_chunks <= 64;
+    const int grid = resident_blocks<kernel>();
+    kb.run = keep ? keep_run(bts, grid) : 0;
+    if (kb.run > 0) return launch_kernel(kernel, grid, kb, stream);
+  }
+  constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, kXmLoad>;
   return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
 }
 

@@ -213,7 +213,9 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
  *                      rows_per_tile, true> (M = 1; dot products on the
  *                      matrix cores; not chosen by the current geometry).
  * Large INT2 launches of one-wave tiles with K >= 8192 take the M = 1
- * kernel's variant that stages the activations per block in LDS.
+ * kernel's variant that stages the activations per block in LDS, those of
+ * 8-row one-batch tiles (K <= 4096) the variant that keeps each wave's
+ * activations across consecutive tiles (both still kind 2).
  * The geometry is chosen per launch, so a problem's result is deterministic
  * for a given launch but may differ in the last bits between a grouped launch
  * and a single one. waves_per_tile must hold `count` ints. */

@@ -662,6 +662,60 @@ def test_grouped_launch_over_several_rounds(torch_gpu, bits, gs, sym, n, k, coun
         assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
 
 
+def test_int2_shared_and_mixed_activations_across_tiles(torch_gpu):
+    """An INT2 launch of one-batch 8-row tiles over more than two rounds of
+    the grid, the case where each wave runs a contiguous range of tiles and
+    reuses the activations of its previous tile when the next one reads the
+    same columns of the same x: problems share one x tensor (consecutive and
+    not), one reads only the first half of that tensor as a K = 2048 problem
+    (same pointer, other columns: must load again), others have their own x,
+    and row counts are ragged. Every problem against the oracle (sampled rows
+    including its last 40) and against its single call."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    gen = torch.Generator(device="cuda").manual_seed(2024)
+    cfg = QuantConfig(2, 64, False, "sequential")
+    x_a16, x_b16, x_c16 = (activations(1, 4096, seed=s) for s in (301, 302, 303))
+    x_a, x_b, x_c = (to_gpu(torch, v) for v in (x_a16, x_b16, x_c16))
+    # (rows, x source, K): 'a2' = the first 2048 columns of x_a (a view, same data pointer)
+    plan = [(6000, "a", 4096), (5003, "a", 4096), (4000, "a2", 2048), (7001, "b", 4096), (6003, "a", 4096),
+            (2000, "a2", 2048), (8000, "c", 4096), (7999, "c", 4096), (5000, "b", 4096), (6000, "a", 4096),
+            (3005, "a2", 2048), (12000, "b", 4096), (7000, "c", 4096)]
+    srcs = {"a": (x_a, x_a16), "b": (x_b, x_b16), "c": (x_c, x_c16),
+            "a2": (x_a[:, :2048], x_a16[:, :2048].copy())}
+    pws, cases, xs, x16s = [], [], [], []
+    for i, (n, src, k) in enumerate(plan):
+        pw = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02, cfg)
+        rng = np.random.Generator(np.random.PCG64(400 + i))
+        rows = np.unique(np.concatenate([rng.choice(n - 40, 160, replace=False), np.arange(n - 40, n)]))
+        qw, sc, ze = pw.qweight.cpu().numpy(), pw.scales.cpu().numpy(), pw.zeros.cpu().numpy()
+        cases.append(OracleCase(pw, qw, sc, ze, rows, deq_ref=False))
+        xs.append(srcs[src][0])
+        x16s.append(srcs[src][1])
+        pws.append(pw)
+    assert xs[2].data_ptr() == x_a.data_ptr() and xs[2].is_contiguous()
+    # the variant's preconditions: 8-row tiles, one wave per tile; 2469 block-tiles
+    # against a grid of 4 blocks per CU (two rounds on a 256-CU device)
+    import ctypes
+
+    from dequant_project_amd import _native
+    arr = (_native.DqGemvProblem * len(plan))()
+    for i, (n, _, k) in enumerate(plan):
+        arr[i].N, arr[i].K, arr[i].group_size = n, k, 64
+    wk, rows_per_tile, kind = (ctypes.c_int * len(plan))(), ctypes.c_int(), ctypes.c_int()
+    assert _native.capi().dq_gemv_plan(arr, len(plan), 1, 2, wk, ctypes.byref(rows_per_tile), ctypes.byref(kind)) == 0
+    assert (list(wk), rows_per_tile.value, kind.value) == ([1] * len(plan), 8, 2)
+    assert sum((n + 7) // 8 for n, _, _ in plan) // 4 >= 2 * 4 * 256
+    ys = ext().gemv_batched(xs, [p.qweight for p in pws], [p.scales for p in pws], [p.zeros for p in pws], 2,
+                            [p.config.effective_group_size(p.shape[1]) for p in pws], False, False)
+    for i, (x, pw) in enumerate(zip(xs, pws)):
+        cases[i].check(ys[i].cpu().numpy(), x16s[i], f"INT2 {plan[i]} problem {i}")
+        single = ext().gemv(x, *ext_args(pw)).float()
+        diff = (ys[i].float() - single).norm() / single.norm().clamp_min(1e-30)
+        assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
+
+
 def test_launch_event_hook_times_the_kernel(torch_gpu):
     torch = torch_gpu
     from dequant_project_amd import _native
