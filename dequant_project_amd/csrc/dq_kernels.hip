@@ -828,7 +828,7 @@ gemv_m1_kernel(const KernelBatch b) {
   int p = 0;
   // block-tiles in runs of `run` consecutive ones, the runs strided over the
   // grid: run = 1 is the plain grid-stride walk. KEEP walks runs of b.run
-  // (2 or 3), so a wave's consecutive tiles are neighbours while the
+  // (kKeepRun), so a wave's consecutive tiles are neighbours while the
   // block-tiles in flight across the chip stay one compact span of the launch
   // (a contiguous share per block spread them over the whole launch and cost
   // 7.7% on the C4 INT2 stack before any reuse)
@@ -1894,32 +1894,33 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
 // Activations staged per block in LDS (gemv_m1_kernel<..., kXmStage>) for
 // INT2, whose lanes load as many activation bytes as weight bytes, in
 // launches where every tile is one wave wide, a tile holds at least two
-// batches (K >= 8192) and the persistent grid walks at least kXlRounds rounds
-// of block-tiles (the variant holds three waves per SIMD, not four).
-// Measured: C5 stack (K = 8192 / 28672 MLP) +7%; K = 4096 tiles of one batch
-// no change; a 2.3-round decode launch -4% (hence the rounds floor); the
-// same staging on every multi-round INT4 launch: INT4 stack -2.6%.
+// batches (K >= 8192) and the persistent grid walks at least xl_rounds(R)
+// rounds of block-tiles. Measured: C5 stack (K = 8192 / 28672 MLP) +7%;
+// K = 4096 tiles of one batch no change; the same staging on every
+// multi-round INT4 launch: INT4 stack -2.6%. The rounds floor was 4 while the
+// 8-row variant held three waves per SIMD (a 2.3-round decode launch then
+// lost 4%); it now holds four, as the unstaged kernel does, and a floor of 2
+// took the C4 INT2 stack's two-round K = 14336 launches too (+2.2% on that
+// stack). The 4-row variant still holds one wave per SIMD fewer than its
+// unstaged kernel and keeps the floor of 4.
 constexpr bool m1_stages_x(int bits) { return bits == 2; }
-constexpr int kXlRounds = 4;
+constexpr int xl_rounds(int R) { return R == 8 ? 2 : 4; }
 
 // Activations kept across tiles (gemv_m1_kernel<..., kXmKeep>) for INT2
-// launches of 8-row, one-batch tiles (K <= 4096, one wave per tile): the grid
-// walks runs of `run` consecutive block-tiles, the longest run of 3 or 2 that
-// still gives every resident block at least one run (shorter launches keep
-// the plain walk). A wave's tiles within a run mostly read the same x. (The
-// variant's 33 KiB of LDS per block allow four waves per SIMD: the 8-row
-// tiles' register count allows no more, the 4-row tiles' six.) Measured on
-// the C4 INT2 stack: with the activation loads removed altogether (a timing
-// copy) 12.6% faster; runs of 3 on its 3488-block-tile launches (1.1 rounds
-// of runs) 31.8 -> 29.1 us, on its 2752-block-tile launches (0.9 rounds)
-// unchanged; runs of 4 over the whole stack +0.9%, one contiguous share per
-// block +0.4% (the walk alone -7.7%).
+// launches of 8-row, one-batch tiles (K <= 4096, one wave per tile) of at
+// least kKeepRounds rounds of block-tiles: the grid walks runs of kKeepRun
+// consecutive block-tiles, and a wave's tiles within a run mostly read the
+// same x. (The variant's 33 KiB of LDS per block allow four waves per SIMD:
+// the 8-row tiles' register count allows no more, the 4-row tiles' six.)
+// Measured on the C4 INT2 stack (2752- and 3488-block-tile launches, 2.7 and
+// 3.4 rounds): with the activation loads removed altogether (a timing copy)
+// 12.6% faster; runs of 3 +4-5% over the plain kernel (the 3488-block-tile
+// launches 31.8 -> 29.1 us), runs of 2 on the shorter launches 0.8% less,
+// runs of 4 +0.9%, one contiguous share per block +0.4% (that walk alone
+// -7.7%).
 constexpr bool m1_keeps_x(int bits) { return bits == 2; }
-int keep_run(int bts, int grid) {
-  for (int run = 3; run >= 2; --run)
-    if (bts >= run * grid) return run;
-  return 0;
-}
+constexpr int kKeepRun = 3;
+constexpr int kKeepRounds = 2;
 
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
@@ -1934,15 +1935,15 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
     bool stage = true;
     for (int i = 0; i < count; ++i) stage = stage && wks[i] == 1 && kb.p[i].n_chunks >= 2 * 64;
     const int grid = resident_blocks<kernel>();
-    if (stage && bts >= kXlRounds * grid) return launch_kernel(kernel, grid, kb, stream);
+    if (stage && bts >= xl_rounds(R) * grid) return launch_kernel(kernel, grid, kb, stream);
   }
   if constexpr (m1_keeps_x(BITS) && PRO == kProNone && !m1_uses_mfma(BITS) && R == 8) {
     constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, false, PRO, kXmKeep>;
     bool keep = true;
     for (int i = 0; i < count; ++i) keep = keep && wks[i] == 1 && kb.p[i].n_chunks <= 64;
     const int grid = resident_blocks<kernel>();
-    kb.run = keep ? keep_run(bts, grid) : 0;
-    if (kb.run > 0) return launch_kernel(kernel, grid, kb, stream);
+    kb.run = kKeepRun;
+    if (keep && bts >= kKeepRounds * grid) return launch_kernel(kernel, grid, kb, stream);
   }
   constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, kXmLoad>;
   return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
