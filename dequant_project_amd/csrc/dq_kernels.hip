@@ -444,30 +444,10 @@ __device__ __forceinline__ void x_pairs_pro(XRaw<BITS, PRO>& R, h2 (&xr)[4][Fmt<
 // Reduce the R per-lane partial sums of a tile and store y. Block-wide LDS
 // combine when the tile's K is split over wk > 1 waves (`part` is this
 // iteration's half of a double buffer, so one barrier per tile suffices).
-// The R consecutive outputs of a tile held by one lane, stored with one
-// 8- or 16-byte store when the tile is whole and y is aligned for it (one
-// memory instruction instead of R two-byte stores from a single lane: those
-// were a third of the M = 1 kernel's memory instructions on 2 KiB rows).
-template <int R>
-__device__ __forceinline__ void store_row_block(uint16_t* y, int row0, int N, const float (&v)[R]) {
-  static_assert(R == 4 || R == 8, "rows per tile");
-  uint16_t* dst = y + row0;
-  if (row0 + R <= N && (reinterpret_cast<uintptr_t>(dst) & (2 * R - 1)) == 0) {
-    uint32_t w[R / 2];
-#pragma unroll
-    for (int i = 0; i < R / 2; ++i)
-      w[i] = static_cast<uint32_t>(f32_to_f16_rn(v[2 * i])) | (static_cast<uint32_t>(f32_to_f16_rn(v[2 * i + 1])) << 16);
-    if constexpr (R == 8)
-      *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
-    else
-      *reinterpret_cast<u32x2*>(dst) = u32x2{w[0], w[1]};
-  } else {
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (row0 + r < N) dst[r] = f32_to_f16_rn(v[r]);
-  }
-}
-
+// After wave_sum_rows the tile's R outputs sit R/4 to a lane in lanes
+// 15, 31, 47 and 63, which store them with one instruction (four lanes, one
+// 4-byte store each at R = 8): R two-byte stores from a single lane were a
+// third of the M = 1 kernel's memory instructions on 2 KiB rows.
 // Rows r .. r + Q - 1 of y from one lane (Q = 1 or 2): one 4-byte store when
 // both rows exist and y + r is aligned for it.
 template <int Q>
@@ -700,22 +680,28 @@ __device__ __forceinline__ float inv_rms(float ssq, int K, float eps) {
 template <int R>
 __device__ __forceinline__ void finish_tile_rms(const KernelProblem& d, const TilePos& t, int wave, int lane, float eps,
                                                 const float (&yacc)[R], float ssq, float (*part)[R + 1]) {
-  float v[R + 1];
+  constexpr int Q = R / 4;  // rows per holder lane 16 g + 15, from row g Q of the tile
+  float v[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) v[r] = yacc[r];
-  v[R] = ssq;
-  wave_sum_lane63<R + 1>(v);
+  wave_sum_rows<R>(v);
+  float sq[1] = {ssq};
+  wave_sum_lane63<1>(sq);  // the wave's sum(x^2) in lane 63, then in every lane
+  const float q = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sq[0]), 63));
+  const bool holder = (lane & 15) == 15;
+  const int g = lane >> 4;
   if (t.wk == 1) {
-    const float f = inv_rms(v[R], d.K, eps);
-    float o[R];
+    const float f = inv_rms(q, d.K, eps);
+    float o[Q];
 #pragma unroll
-    for (int r = 0; r < R; ++r) o[r] = v[r] * f;
-    if (t.active && lane == 63) store_row_block<R>(d.y, t.row0, d.N, o);
+    for (int i = 0; i < Q; ++i) o[i] = v[i] * f;
+    if (t.active && holder) store_rows<Q>(d.y, t.row0 + g * Q, d.N, o);
   } else {
-    if (lane == 63) {
+    if (holder) {
 #pragma unroll
-      for (int i = 0; i <= R; ++i) part[wave][i] = v[i];
+      for (int i = 0; i < Q; ++i) part[wave][g * Q + i] = v[i];
     }
+    if (lane == 63) part[wave][R] = q;
     __syncthreads();  // all 4 waves of the block run the same block-tile sequence
     if (t.active && t.kw == 0 && lane < R) {
       float a = 0.f, q = 0.f;
