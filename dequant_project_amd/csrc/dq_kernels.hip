@@ -1885,12 +1885,13 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
 // K = 4096 tiles of one batch no change; the same staging on every
 // multi-round INT4 launch: INT4 stack -2.6%. The rounds floor was 4 while the
 // 8-row variant held three waves per SIMD (a 2.3-round decode launch then
-// lost 4%); it now holds four, as the unstaged kernel does, and a floor of 2
+// lost 4%); it now holds four, as the unstaged kernel does. A floor of 2
 // took the C4 INT2 stack's two-round K = 14336 launches too (+2.2% on that
-// stack). The 4-row variant still holds one wave per SIMD fewer than its
+// stack), one of 1 also C5 decode's 1.75-round gate | up launches (C5 decode
+// +3.5%). The 4-row variant still holds one wave per SIMD fewer than its
 // unstaged kernel and keeps the floor of 4.
 constexpr bool m1_stages_x(int bits) { return bits == 2; }
-constexpr int xl_rounds(int R) { return R == 8 ? 2 : 4; }
+constexpr int xl_rounds(int R) { return R == 8 ? 1 : 4; }
 
 // Activations kept across tiles (gemv_m1_kernel<..., kXmKeep>) for INT2
 // launches of 8-row, one-batch tiles (K <= 4096, one wave per tile) of at
