@@ -17,34 +17,55 @@ structures are timed:
               launches of up to 16 problems of equal K -- 12 launches of six
               K=4096 projections x 16/6 layers, 2 of 16 down_proj -- i.e. the
               sustained bandwidth of the kernel over the Llama-3-8B layer
-              shapes, with launch overhead amortized (the reference times
-              independent back-to-back GEMV calls the same way,
-              scripts/bench_dequant_kernel.py:119-168);
+              shapes (the reference times independent back-to-back GEMV calls
+              the same way, scripts/bench_dequant_kernel.py:119-168);
   decode      what a decoder launches given a Llama layer's data
               dependencies: q|k|v grouped (same input), o, gate|up grouped,
               down -- 4 launches per layer, 128 per step;
   per_linear  the QuantLinear drop-in path: one launch per projection.
 
-Printed: ONE JSON line on stdout (progress goes to stderr).
-  value       stack-mode algorithmic bytes per step / step time, GB/s (the
-              byte_model accounting: packed weights + scales + zeros + x + y)
-  roofline    the dominant kernel instance of the stack step: algorithmic
-              bytes per launch / its mean launch duration, the latter from HIP
-              events around the timed graph replays divided by the launches
-              (the stack step runs one kernel instance), against 8 TB/s
-  cpu_baseline  the reference's CPU torch path (oracle/cpu_path.py) on one
-              layer of the same stack, on this host's cores
-  other_format_stacks / batch_stacks  the same stack step in INT8 and INT2,
-              and the INT4 stack at M = 2, 4, 8 (C4's other batch sizes)
-  gemm_small_stacks  the fused small GEMM over the stack at M = 16, 64, with
-              the reference's dequantize + F.linear timed beside it
-  decode_with_fused_prologues  the decode launches with RMSNorm / SwiGLU
-              fused in, against the same launches without
-  c5_llama3_70b_stack  BASELINE.json's C5: the Llama-3-70B shapes, INT4
-              attention, INT2 MLP, INT8 lm_head (~25 GB), stack and decode
-              launch structures
+Measurement protocol (why the timed replays see the steady state):
+  * Every input of the timed legs is built and every graph captured before
+    any timing starts, and nothing is freed until the end. Freeing device
+    memory (torch.cuda.empty_cache) lets the driver clear the freed VRAM in
+    the background, which costs the next ~10 ms per freed GB about 3% of the
+    bandwidth; graph capture and host-side building leave the GPU idle, after
+    which the power management takes ~20 ms of load to bring the memory path
+    back to its steady clocks (the first replays then run up to 15% slower).
+  * The timed legs then run back to back on one stream with no host
+    synchronization between them. The first leg is the streaming-read
+    ceiling (a measurement of its own, reported below, long enough to cover
+    that ramp); the headline stack follows immediately with its W warm-up
+    and K timed replays.
+  * roofline.achieved is the dominant kernel's own duration: after the timed
+    legs, the headline's launches run eagerly STEPS times with the engine's
+    launch-event hook (hipExtLaunchKernelGGL start/stop events on the launch
+    stream), i.e. the figure rocprofv3's kernel trace reports.
 
-  python bench.py [--gpus 1] [--steps 20] [--warmup 100]
+Printed: ONE JSON line on stdout (progress goes to stderr).
+  value            stack-mode algorithmic bytes per step / step time, GB/s
+                   (the byte_model accounting: packed weights + scales +
+                   zeros + x + y)
+  roofline         the headline's kernel: algorithmic bytes per launch / its
+                   mean kernel duration; traffic from the committed rocprofv3
+                   FETCH_SIZE + WRITE_SIZE summary of that kernel (static)
+  ceilings         measured streaming-read ceiling and empty-kernel gap
+  cpu_baseline     the reference's CPU torch path (oracle/cpu_path.py) on the
+                   host cores: C4 one layer (value), rows for C1-C5, 1 thread
+  other_format_stacks / batch_stacks  the same stack step in INT8 and INT2,
+                   and the INT4 stack at M = 2, 4, 8 (C4's other batch sizes)
+  gemm_small_stacks  the fused small GEMM over the stack at M = 16, 64, with
+                   the reference's dequantize + F.linear timed beside it
+  decode_with_fused_prologues  the decode launches with RMSNorm / SwiGLU
+                   fused in, against the same launches without
+  c5_llama3_70b_stack  BASELINE.json's C5 (~25 GB), stack and decode
+  single_configs   C1, C2 (M = 1, 4), C3, each in a graph of distinct copies
+  format_axis      the reference's microbenchmark table on the C4 shapes: per
+                   shape and format, per-call time in a graph of distinct
+                   copies, with fp16 F.linear and the speed-up over it
+                   (scripts/bench_dequant_kernel.py:61-78, 119-168)
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
 
 import argparse
@@ -70,6 +91,14 @@ PROJS = [("q_proj", HIDDEN, HIDDEN), ("k_proj", KV, HIDDEN), ("v_proj", KV, HIDD
 GROUPS = [("qkv", ("q_proj", "k_proj", "v_proj")), ("o", ("o_proj",)),
           ("gate_up", ("gate_proj", "up_proj")), ("down", ("down_proj",))]
 MALL_BYTES = 256 * 2 ** 20
+CEILING_BYTES = 4 * 2 ** 30      # streaming-read ceiling buffer
+CEILING_WARM, CEILING_REPS = 20, 40
+EMPTY_LAUNCHES = 1000
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_m1_pipe_kernel_int4_c4_stack_traffic.md")
+
+# a Llama-3-70B-shape stack in mixed precision
+C5_LAYERS = 80
+C5_HIDDEN, C5_KV, C5_INTER, C5_VOCAB = 8192, 1024, 28672, 128256
 
 
 def log(*a):
@@ -87,12 +116,11 @@ def parse_args():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # ~70 ms of replays: the GPU needs ~45 ms of this load after the stack is
-    # built before the step time settles (the first replays run ~15% slower)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=LAYERS, help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the C1/C2/C3 single-config runs")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="time the C4 INT4 modes only (no other formats, batches, C5, single configs, format axis)")
     ap.add_argument("--modes", default="stack,decode,per_linear",
                     help="comma-separated step structures to time (stack is the headline)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -101,8 +129,9 @@ def parse_args():
 
 
 class Engine:
-    """The engine's entry points used here: the torch extension for launches
-    and the C ABI's launch plan (to name the kernel instance of a launch)."""
+    """The engine's entry points used here: the torch extension for launches,
+    the C ABI for the launch plan (kernel instance names), the launch-event
+    hook and the measurement kernels."""
 
     def __init__(self, torch):
         from dequant_project_amd import _native
@@ -139,34 +168,47 @@ class Engine:
         fmt = f"{cfg.bits}, {str(cfg.symmetric).lower()}, {str(cfg.layout == 'interleaved').lower()}"
         if kind.value == 1:
             return f"gemv_quad_kernel<{fmt}, {rows.value // 4}, {1 if m <= 4 else 2}>", tuple(wk)
+        if kind.value == 4:
+            return f"gemv_m1_pipe_kernel<{fmt}, {rows.value}>", tuple(wk)
         return f"gemv_m1_kernel<{fmt}, {rows.value}, {'true' if kind.value == 3 else 'false'}>", tuple(wk)
+
+    def stream(self):
+        return self.torch.cuda.current_stream().cuda_stream
+
+    def stream_read(self, buf, sink):
+        self.native.check(self.capi.dq_stream_read(buf.data_ptr(), buf.numel() * buf.element_size(),
+                                                   sink.data_ptr(), self.stream()))
+
+    def empty_kernel(self):
+        self.native.check(self.capi.dq_empty_kernel(self.stream()))
+
+
+# ----------------------------------------------------------------- building
+def quantize_random(torch, gen, n, k, cfg):
+    from dequant_project_amd.packer import quantize_tensor
+
+    w = torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02
+    pw = quantize_tensor(w, cfg)
+    del w
+    return pw
 
 
 def build_stack(torch, layers, seed=20251201, cfg=None):
-    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+    from dequant_project_amd.packer import QuantConfig
 
     cfg = cfg or QuantConfig(4, 128, False, "sequential")
     gen = torch.Generator(device="cuda").manual_seed(seed)
-    stack = []
-    for _ in range(layers):
-        layer = {}
-        for name, n, k in PROJS:
-            w = torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02
-            layer[name] = quantize_tensor(w, cfg)
-            del w
-        stack.append(layer)
+    stack = [{name: quantize_random(torch, gen, n, k, cfg) for name, n, k in PROJS} for _ in range(layers)]
     return cfg, stack, make_xs(torch, layers, 1, gen)
 
 
 def make_xs(torch, layers, m, gen):
     """Per layer, the fp16 N(0, 1) inputs [m, K] of its four launch roles."""
-    xs = []
-    for _ in range(layers):
-        xs.append({"qkv": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-                   "o": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-                   "gate_up": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-                   "down": torch.randn(m, INTER, generator=gen, device="cuda", dtype=torch.float16)})
-    return xs
+    return [{"qkv": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+             "o": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+             "gate_up": torch.randn(m, HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+             "down": torch.randn(m, INTER, generator=gen, device="cuda", dtype=torch.float16)}
+            for _ in range(layers)]
 
 
 def step_launches(stack, xs, mode):
@@ -203,6 +245,15 @@ def launch_bytes(xs, pws):
     return total
 
 
+def kernel_instances(eng, launches):
+    """Kernel instance of every launch of a step (dq_gemv_plan) -> {name: [bytes...]}."""
+    inst = {}
+    for _, x, p in launches:
+        name, _ = eng.kernel_name(x, p)
+        inst.setdefault(name, []).append(launch_bytes(x, p))
+    return inst
+
+
 def capture(torch, fn):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -216,115 +267,154 @@ def capture(torch, fn):
     return g
 
 
-def time_graph(torch, graph, steps, warmup):
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    evs[0].record()
-    for i in range(steps):
-        graph.replay()
-        evs[i + 1].record()
-    torch.cuda.synchronize()
-    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
-    return evs[0].elapsed_time(evs[-1]) / steps, per
+# ------------------------------------------------------------------ timing
+class Leg:
+    """One timed leg: a captured graph replayed `warmup` times, then `steps`
+    times between events. Replays are only enqueued here; `result` reads the
+    events after the single synchronization that ends the timed phase."""
+
+    def __init__(self, torch, name, graph, steps, warmup, step_bytes=None, meta=None, layers=None):
+        self.torch, self.name, self.graph = torch, name, graph
+        self.steps, self.warmup = steps, warmup
+        self.step_bytes, self.meta, self.layers = step_bytes, meta or {}, layers
+        self.evs = None
+
+    def enqueue(self):
+        for _ in range(self.warmup):
+            self.graph.replay()
+        self.evs = [self.torch.cuda.Event(enable_timing=True) for _ in range(self.steps + 1)]
+        self.evs[0].record()
+        for i in range(self.steps):
+            self.graph.replay()
+            self.evs[i + 1].record()
+
+    def result(self):
+        per = [self.evs[i].elapsed_time(self.evs[i + 1]) for i in range(self.steps)]
+        ms = self.evs[0].elapsed_time(self.evs[-1]) / self.steps
+        out = {"ms_per_step": ms, "step_ms": summarize(per)}
+        if self.step_bytes:
+            out.update(bytes_per_step=self.step_bytes, gbs=self.step_bytes / (ms * 1e-3) / 1e9,
+                       pct_peak=100 * self.step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS)
+        if self.layers:
+            out["us_per_layer"] = ms * 1e3 / self.layers
+        out.update(self.meta)
+        return out
 
 
-def run_mode(torch, eng, stack, xs, mode, steps, warmup):
-    launches = step_launches(stack, xs, mode)
+def gemv_leg(torch, eng, name, launches, steps, warmup, layers):
     step_bytes = sum(launch_bytes(x, p) for _, x, p in launches)
 
     def fn():
         for _, x, p in launches:
             eng.gemv_group(x, p)
 
-    graph = capture(torch, fn)
-    ms, per = time_graph(torch, graph, steps, warmup)
-    del graph
-    return launches, step_bytes, ms, per
+    meta = {"launches_per_step": len(launches),
+            "kernel_instances": {k: len(v) for k, v in kernel_instances(eng, launches).items()}}
+    return Leg(torch, name, capture(torch, fn), steps, warmup, step_bytes, meta, layers)
 
 
-def kernel_instances(eng, launches):
-    """Kernel instance of every launch of a step (dq_gemv_plan) -> {name: [bytes...]}."""
-    inst = {}
-    for _, x, p in launches:
-        name, _ = eng.kernel_name(x, p)
-        inst.setdefault(name, []).append(launch_bytes(x, p))
-    return inst
-
-
-def cpu_baseline(torch, stack):
-    """The reference's CPU torch path (unpack -> dequantize -> fp32 F.linear) on layer 0."""
-    from oracle import cpu_path
-
-    layer = stack[0]
-    cpu = {n: (p.qweight.cpu(), p.scales.cpu(), p.zeros.cpu(), p.config, p.shape) for n, p in layer.items()}
-    gen = torch.Generator().manual_seed(3)
-    xs = {n: torch.randn(1, shape[1], generator=gen, dtype=torch.float16) for n, (*_, shape) in cpu.items()}
-    layer_bytes = sum(launch_bytes([xs[n]], [p]) for n, p in layer.items())
-
-    def one_layer(matmul_only=None):
-        for n, (qw, sc, ze, c, shape) in cpu.items():
-            if matmul_only is None:
-                cpu_path.gemv(xs[n], qw, sc, ze, c.bits, c.effective_group_size(shape[1]), c.symmetric,
-                              c.layout == "interleaved")
-            else:
-                torch.nn.functional.linear(xs[n].float(), matmul_only[n])
-
-    threads = torch.get_num_threads()
-    t0 = time.perf_counter()
-    one_layer()  # warm-up
-    warm = time.perf_counter() - t0
-    reps = max(3, min(20, int(15.0 / max(warm, 1e-3))))
-    samples = []
+def kernel_durations(torch, eng, launches, reps):
+    """Per-launch kernel durations (us) of `launches`, run eagerly `reps` times,
+    each launch timed by the engine's launch-event hook (the start/stop events
+    bracket the kernel on its own stream)."""
+    lib = eng.capi
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in launches]
+    for a, b in evs:  # an event's handle exists once it has been recorded
+        a.record()
+        b.record()
+    out = []
     for _ in range(reps):
-        t0 = time.perf_counter()
-        one_layer()
-        samples.append(time.perf_counter() - t0)
-    med = statistics.median(samples)
-    weights = {n: cpu_path.dequantize(qw, sc, ze, c.bits, c.effective_group_size(shape[1]), c.symmetric,
-                                      c.layout == "interleaved", shape[1]).float()
-               for n, (qw, sc, ze, c, shape) in cpu.items()}
-    mm = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        one_layer(weights)
-        mm.append(time.perf_counter() - t0)
-    return {"value": layer_bytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": (f"one Llama-3-8B layer (7 linears, {layer_bytes / 1e6:.1f} MB packed INT4 g128 asym, M=1) "
-                       f"of the benchmark stack, unpack -> dequantize -> fp32 F.linear "
-                       f"(oracle/cpu_path.py), median of {reps} after 1 warm-up"),
-            "us_per_layer": med * 1e6, "matmul_only_us_per_layer": statistics.median(mm) * 1e6,
-            "os_cpu_count": os.cpu_count()}
+        for (a, b), (_, x, p) in zip(evs, launches):
+            eng.native.check(lib.dq_set_launch_events(a.cuda_event, b.cuda_event))
+            eng.gemv_group(x, p)
+        torch.cuda.synchronize()
+        out.append([a.elapsed_time(b) * 1e3 for a, b in evs])
+    return out
 
 
-def single_config(torch, eng, name, n, k, cfg, m, reps=10):
-    """The reference's rotating-copy microbenchmark for one shape (working set
-    >= 8 x the 256 MB Infinity Cache): per-call graph time and kernel time."""
-    from dequant_project_amd.packer import quantize_tensor
+def profiled_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-calibrated), or None if that summary is of
+    another kernel."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+        rec = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
+    except (OSError, IndexError, ValueError):
+        return None, None
+    if rec.get("kernel") != kernel:
+        return None, None
+    return rec["traffic_bytes_per_launch"], rec
 
-    gen = torch.Generator(device="cuda").manual_seed(n * 7 + k)
-    first = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02, cfg)
-    copies = max(4, math.ceil(8 * MALL_BYTES / first.nbytes))
-    pws = [first] + [quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02,
-                                     cfg) for _ in range(copies - 1)]
-    x = torch.randn(m, k, generator=gen, device="cuda", dtype=torch.float16)
 
-    def fn():
-        for p in pws:
-            eng.gemv_group([x], [p])
+# ------------------------------------------------------------ extra legs
+def c5_build(torch):
+    """80 layers of q/k/v/o in INT4 g128 asym and gate/up/down in INT2 g64
+    asym, plus an INT8 per-channel sym lm_head 8192 -> 128256 (~25 GB
+    packed), from seeded fp16 N(0, 0.02) weights quantized on the GPU one
+    tensor at a time; x fp16 N(0, 1), batch 1."""
+    from dequant_project_amd.packer import QuantConfig
 
-    graph = capture(torch, fn)
-    ms, per = time_graph(torch, graph, reps, 2)
-    b = launch_bytes([x], [first])
-    us = statistics.median(per) * 1e3 / copies
-    res = {"shape": [n, k], "M": m, "format": f"INT{cfg.bits} g{cfg.group_size or 'pc'} "
-           f"{'sym' if cfg.symmetric else 'asym'}", "copies": copies, "bytes_per_call": b,
-           "us_per_call": us, "gbs": b / (us * 1e-6) / 1e9, "pct_peak": 100 * b / (us * 1e-6) / 1e9 / PEAK_GBS,
-           "kernel": eng.kernel_name([x], [first])[0]}
-    del graph, pws, first
-    torch.cuda.empty_cache()
-    return name, res
+    attn, mlp, head = QuantConfig(4, 128, False), QuantConfig(2, 64, False), QuantConfig(8, None, True)
+    gen = torch.Generator(device="cuda").manual_seed(20251206)
+    shapes = {"q_proj": (C5_HIDDEN, C5_HIDDEN, attn), "k_proj": (C5_KV, C5_HIDDEN, attn),
+              "v_proj": (C5_KV, C5_HIDDEN, attn), "o_proj": (C5_HIDDEN, C5_HIDDEN, attn),
+              "gate_proj": (C5_INTER, C5_HIDDEN, mlp), "up_proj": (C5_INTER, C5_HIDDEN, mlp),
+              "down_proj": (C5_HIDDEN, C5_INTER, mlp)}
+    stack = [{name: quantize_random(torch, gen, n, k, c) for name, (n, k, c) in shapes.items()}
+             for _ in range(C5_LAYERS)]
+    lm_head = quantize_random(torch, gen, C5_VOCAB, C5_HIDDEN, head)
+    xs = [{"qkv": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+           "o": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+           "gate_up": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
+           "down": torch.randn(1, C5_INTER, generator=gen, device="cuda", dtype=torch.float16)} for _ in stack]
+    x_head = torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16)
+    return stack, lm_head, xs, x_head
+
+
+def c5_launches(stack, lm_head, xs, x_head):
+    """Grouped launches of equal format and K ("stack") and the decoder's
+    launches ("decode": q|k|v, o, gate|up, down per layer), then the lm_head."""
+    groups = {}
+    for layer, x in zip(stack, xs):
+        for role, names in GROUPS:
+            for n in names:
+                p = layer[n]
+                groups.setdefault((p.config.bits, p.shape[1]), []).append((x[role], p))
+    out = {"stack": [("g", [c[0] for c in items[i:i + 16]], [c[1] for c in items[i:i + 16]])
+                     for items in groups.values() for i in range(0, len(items), 16)],
+           "decode": [(role, [x[role]] * len(names), [layer[n] for n in names])
+                      for layer, x in zip(stack, xs) for role, names in GROUPS]}
+    for mode in out:
+        out[mode].append(("lm_head", [x_head], [lm_head]))
+    return out
+
+
+# name, N, K, (bits, group_size, symmetric), M
+SINGLE_CONFIGS = [("C1", 4096, 4096, (4, 128, False), 1), ("C2", 11008, 4096, (8, None, True), 1),
+                  ("C2_M4", 11008, 4096, (8, None, True), 4), ("C3", 4096, 11008, (2, 64, False), 1)]
+
+
+def single_copies(torch, n, k, cfg, seed, outliers=False):
+    """The reference's rotating-copy working set (>= 8 x the 256 MB Infinity
+    Cache in place of its L2, and at least one copy per layer,
+    scripts/bench_dequant_kernel.py:119-126): one seeded weight quantized,
+    then cloned into distinct device copies (the timing depends on the
+    memory, not on the values)."""
+    from dequant_project_amd.packer import PackedWeight, quantize_tensor
+
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02
+    if outliers:  # C3: 0.1% of the entries at +-10 sigma
+        cnt = max(1, (n * k) // 1000)
+        idx = torch.randint(0, n * k, (cnt,), generator=gen, device="cuda")
+        sign = torch.where(torch.rand(cnt, generator=gen, device="cuda") < 0.5, -1.0, 1.0)
+        w.view(-1)[idx] = (sign * 0.2).to(torch.float16)
+    first = quantize_tensor(w, cfg)
+    del w
+    copies = max(LAYERS, math.ceil(8 * MALL_BYTES / first.nbytes))
+    return [first] + [PackedWeight(first.qweight.clone(), first.scales.clone(),
+                                   None if first.zeros is None else first.zeros.clone(), first.config, first.shape)
+                      for _ in range(copies - 1)]
 
 
 def gemm_stack(torch, stack, m, steps, warmup):
@@ -345,16 +435,14 @@ def gemm_stack(torch, stack, m, steps, warmup):
         for x, p in items:
             gemm_small(x, p)
 
-    graph = capture(torch, fused)
-    ms, per = time_graph(torch, graph, steps, warmup)
-    del graph
+    leg = Leg(torch, f"gemm M={m}", capture(torch, fused), steps, warmup, step_bytes, layers=len(stack))
+    leg.enqueue()
 
     def reference():
         for x, p in items:
             F.linear(x, dequantize_cuda(p))
 
     reference()
-    torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ref = []
     for _ in range(max(3, steps // 4)):
@@ -363,142 +451,160 @@ def gemm_stack(torch, stack, m, steps, warmup):
         b.record()
         torch.cuda.synchronize()
         ref.append(a.elapsed_time(b))
+    r = leg.result()
     ref_ms = statistics.median(ref)
-    return {"M": m, "bytes_per_step": step_bytes, "ms_per_step": ms, "step_ms": summarize(per),
-            "gbs": step_bytes / (ms * 1e-3) / 1e9, "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
-            "us_per_layer": ms * 1e3 / len(stack),
-            "dequantize_plus_linear_ms_per_step": ref_ms, "speedup_vs_dequantize_plus_linear": ref_ms / ms}
+    r.update(M=m, dequantize_plus_linear_ms_per_step=ref_ms, speedup_vs_dequantize_plus_linear=ref_ms / r["ms_per_step"])
+    return r
 
 
-def prologue_decode(torch, eng, stack, xs, steps, warmup):
-    """The decode launch structure (q|k|v, o, gate|up, down per layer) with the
-    RMSNorm prologue fused into q|k|v and gate|up and the SwiGLU prologue into
-    down (fused.gemv_rmsnorm / gemv_swiglu), against the same launches without
-    prologues: what the fusion costs inside the GEMVs (the separate norm and
-    SwiGLU kernels it removes are not counted here)."""
-    from dequant_project_amd import fused
-
-    gen = torch.Generator(device="cuda").manual_seed(20251205)
-    gamma = torch.rand(HIDDEN, generator=gen, device="cuda", dtype=torch.float16) + 0.5
-    ups = [torch.randn(1, INTER, generator=gen, device="cuda", dtype=torch.float16) for _ in stack]
-    plain = step_launches(stack, xs, "decode")
-    step_bytes = sum(launch_bytes(x, p) for _, x, p in plain)
-
-    def run_plain():
-        for _, x, p in plain:
-            eng.gemv_group(x, p)
-
-    def run_fused():
-        for li, (layer, x) in enumerate(zip(stack, xs)):
-            fused.gemv_rmsnorm(x["qkv"], gamma, 1e-5, [layer["q_proj"], layer["k_proj"], layer["v_proj"]])
-            eng.gemv_group([x["o"]], [layer["o_proj"]])
-            fused.gemv_rmsnorm(x["gate_up"], gamma, 1e-5, [layer["gate_proj"], layer["up_proj"]])
-            fused.gemv_swiglu(x["down"], ups[li], layer["down_proj"])
-
-    out = {}
-    for name, fn in (("plain", run_plain), ("fused_prologues", run_fused)):
-        graph = capture(torch, fn)
-        ms, per = time_graph(torch, graph, steps, warmup)
-        del graph
-        out[name] = {"ms_per_step": ms, "step_ms": summarize(per), "us_per_layer": ms * 1e3 / len(stack),
-                     "gbs": step_bytes / (ms * 1e-3) / 1e9}
-    out["bytes_per_step"] = step_bytes
-    return out
+# label, (bits, group_size, symmetric, layout) or None for fp16 F.linear
+FORMAT_AXIS = [("fp16 F.linear", None), ("INT8 g128 sym", (8, 128, True, "sequential")),
+               ("INT4 g128 sym", (4, 128, True, "sequential")), ("INT4 g128 asym", (4, 128, False, "sequential")),
+               ("INT4 g32 sym", (4, 32, True, "sequential")), ("INT4 per-chan sym", (4, None, True, "sequential")),
+               ("INT4 g128 sym inter", (4, 128, True, "interleaved"))]
+FORMAT_SHAPES = [("q/o_proj", HIDDEN, HIDDEN), ("k/v_proj", KV, HIDDEN), ("gate/up_proj", INTER, HIDDEN),
+                 ("down_proj", HIDDEN, INTER)]
 
 
-# BASELINE.json config C5: a Llama-3-70B-shape stack in mixed precision
-C5_LAYERS = 80
-C5_HIDDEN, C5_KV, C5_INTER, C5_VOCAB = 8192, 1024, 28672, 128256
+def format_axis(torch, eng, steps, warmup):
+    """The reference's microbenchmark (scripts/bench_dequant_kernel.py:61-78,
+    119-168) on the Llama-3-8B projection shapes: per (shape, format) a graph
+    of n_copies = max(32, ceil(8 x 256 MB / bytes)) back-to-back calls over
+    distinct copies, M = 1; per-call time = replay time / n_copies (median,
+    p25, p75 over the timed replays); fp16 F.linear over the fp16 weight is
+    the row every speed-up is measured against. Every pair is built and
+    captured first, then all are timed back to back."""
+    import torch.nn.functional as F
 
+    from dequant_project_amd import byte_model as bm
+    from dequant_project_amd.packer import PackedWeight, QuantConfig, quantize_tensor
 
-def c5_stack(torch, eng, steps, warmup, layers=C5_LAYERS):
-    """80 layers of q/k/v/o in INT4 g128 asym and gate/up/down in INT2 g64
-    asym, plus an INT8 per-channel sym lm_head 8192 -> 128256 (~25 GB
-    packed), from seeded fp16 N(0, 0.02) weights quantized on the GPU one
-    tensor at a time; x fp16 N(0, 1), batch 1. Timed as grouped launches of
-    equal format and K ("stack") and as a decoder launches them ("decode":
-    q|k|v, o, gate|up, down per layer, then the lm_head)."""
-    from dequant_project_amd.packer import QuantConfig, quantize_tensor
-
-    attn, mlp, head = QuantConfig(4, 128, False), QuantConfig(2, 64, False), QuantConfig(8, None, True)
-    gen = torch.Generator(device="cuda").manual_seed(20251206)
-
-    def q(n, k, cfg):
+    gen = torch.Generator(device="cuda").manual_seed(20251207)
+    pairs = []
+    for label, n, k in FORMAT_SHAPES:
         w = torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02
-        pw = quantize_tensor(w, cfg)
-        del w
-        return pw
+        x = torch.randn(1, k, generator=gen, device="cuda", dtype=torch.float16)
+        for fmt, spec in FORMAT_AXIS:
+            if spec is None:
+                copies = max(LAYERS, math.ceil(8 * MALL_BYTES / (n * k * 2)))
+                ws = [w.clone() for _ in range(copies)]
 
-    t0 = time.perf_counter()
-    stack = []
-    for _ in range(layers):
-        stack.append({"q_proj": q(C5_HIDDEN, C5_HIDDEN, attn), "k_proj": q(C5_KV, C5_HIDDEN, attn),
-                      "v_proj": q(C5_KV, C5_HIDDEN, attn), "o_proj": q(C5_HIDDEN, C5_HIDDEN, attn),
-                      "gate_proj": q(C5_INTER, C5_HIDDEN, mlp), "up_proj": q(C5_INTER, C5_HIDDEN, mlp),
-                      "down_proj": q(C5_HIDDEN, C5_INTER, mlp)})
-    lm_head = q(C5_VOCAB, C5_HIDDEN, head)
+                def fn(ws=ws, x=x):
+                    for wi in ws:
+                        F.linear(x, wi)
+                call_bytes = n * k * 2 + k * 2 + n * 2
+                kernel = "torch F.linear (fp16)"
+            else:
+                cfg = QuantConfig(*spec)
+                first = quantize_tensor(w, cfg)
+                copies = max(LAYERS, math.ceil(8 * MALL_BYTES / first.nbytes))
+                ws = [first] + [PackedWeight(first.qweight.clone(), first.scales.clone(),
+                                             None if first.zeros is None else first.zeros.clone(), cfg, first.shape)
+                                for _ in range(copies - 1)]
+
+                def fn(ws=ws, x=x):
+                    for p in ws:
+                        eng.gemv_group([x], [p])
+                call_bytes = bm.gemv_call_bytes(n, k, cfg.bits, cfg.group_size, cfg.symmetric, 1)
+                kernel = eng.kernel_name([x], [first])[0]
+            leg = Leg(torch, f"{label} {fmt}", capture(torch, fn), steps, warmup)
+            pairs.append((label, n, k, fmt, copies, call_bytes, kernel, leg, ws))
     torch.cuda.synchronize()
-    build_s = time.perf_counter() - t0
-    xs = [{"qkv": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-           "o": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-           "gate_up": torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16),
-           "down": torch.randn(1, C5_INTER, generator=gen, device="cuda", dtype=torch.float16)} for _ in stack]
-    x_head = torch.randn(1, C5_HIDDEN, generator=gen, device="cuda", dtype=torch.float16)
-
-    launches = {}
-    groups = {}
-    for layer, x in zip(stack, xs):
-        for role, names in GROUPS:
-            for n in names:
-                p = layer[n]
-                groups.setdefault((p.config.bits, p.shape[1]), []).append((x[role], p))
-    launches["stack"] = [([c[0] for c in items[i:i + 16]], [c[1] for c in items[i:i + 16]])
-                         for items in groups.values() for i in range(0, len(items), 16)]
-    launches["decode"] = [([x[role]] * len(names), [layer[n] for n in names])
-                          for layer, x in zip(stack, xs) for role, names in GROUPS]
-    for mode in launches:
-        launches[mode].append(([x_head], [lm_head]))
-    out = {"layers": layers, "build_s": build_s}
-    for mode, ls in launches.items():
-        step_bytes = sum(launch_bytes(x, p) for x, p in ls)
-
-        def fn():
-            for x, p in ls:
-                eng.gemv_group(x, p)
-
-        graph = capture(torch, fn)
-        ms, per = time_graph(torch, graph, steps, warmup)
-        del graph
-        out[mode] = {"launches_per_step": len(ls), "bytes_per_step": step_bytes, "ms_per_step": ms,
-                     "step_ms": summarize(per), "gbs": step_bytes / (ms * 1e-3) / 1e9,
-                     "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
-                     "us_per_layer": ms * 1e3 / layers,
-                     "kernel_instances": {k: len(v) for k, v in kernel_instances(eng, [(None, x, p) for x, p in ls]).items()}}
-    del stack, lm_head, launches, groups
-    torch.cuda.empty_cache()
-    return out
+    for p in pairs:
+        p[7].enqueue()
+    torch.cuda.synchronize()
+    rows, base = [], {}
+    for label, n, k, fmt, copies, call_bytes, kernel, leg, _ in pairs:
+        r = leg.result()
+        us = r["step_ms"]["median"] * 1e3 / copies
+        base.setdefault(label, us)
+        rows.append({"shape": label, "format": fmt, "N": n, "K": k, "copies": copies, "bytes_per_call": call_bytes,
+                     "us_median": us, "us_p25": r["step_ms"]["p25"] * 1e3 / copies,
+                     "us_p75": r["step_ms"]["p75"] * 1e3 / copies, "gbs": call_bytes / (us * 1e-6) / 1e9,
+                     "pct_peak": 100 * call_bytes / (us * 1e-6) / 1e9 / PEAK_GBS,
+                     "floor_us": call_bytes / (PEAK_GBS * 1e9) * 1e6, "speedup_vs_fp16": base[label] / us,
+                     "kernel": kernel})
+    return rows
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_m1_kernel_int4_c4_stack_traffic.md")
+# ------------------------------------------------------------ CPU baseline
+def cpu_baseline(torch, c4_layer, singles, c5_layer, budget_s=30.0):
+    """The reference's CPU torch path (oracle/cpu_path.py: unpack -> dequantize
+    -> fp32 F.linear), timed with time.perf_counter on this host's cores
+    (torch.get_num_threads()) per BASELINE.md's protocol: 3 warm-ups, then the
+    median and p25/p75 of up to 20 repetitions (fewer for rows whose single
+    repetition would overrun the time budget; the count is recorded),
+    'dequant + matmul' and 'matmul only' (the fp32 weight materialized
+    beforehand). C4 and C5 time one layer (7 linears; the C5 row excludes the
+    lm_head) and scale by the layer count; a 1-thread row repeats C1.
+    value = the C4 layer's GB/s."""
+    from oracle import cpu_path
 
+    def host(p):
+        return (p.qweight.cpu(), p.scales.cpu(), None if p.zeros is None else p.zeros.cpu(), p.config, p.shape)
 
-def profiled_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (copy-calibrated), or None if that summary is of
-    another kernel."""
+    def row(name, items, m, layers, reps_cap, warm):
+        gen = torch.Generator().manual_seed(3)
+        ws = [host(p) for p in items]
+        xs = [torch.randn(m, shape[1], generator=gen, dtype=torch.float16) for *_, shape in ws]
+        nbytes = sum(launch_bytes([x], [p]) for x, p in zip(xs, items))
+
+        def deq_mm():
+            for x, (qw, sc, ze, c, shape) in zip(xs, ws):
+                cpu_path.gemv(x, qw, sc, ze, c.bits, c.effective_group_size(shape[1]), c.symmetric,
+                              c.layout == "interleaved")
+
+        t0 = time.perf_counter()
+        deq_mm()
+        one = time.perf_counter() - t0
+        for _ in range(warm - 1):
+            deq_mm()
+        reps = int(max(3, min(reps_cap, budget_s / 8 / max(one, 1e-4))))
+        samples = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            deq_mm()
+            samples.append(time.perf_counter() - t0)
+        wf = [cpu_path.dequantize(qw, sc, ze, c.bits, c.effective_group_size(shape[1]), c.symmetric,
+                                  c.layout == "interleaved", shape[1]).float() for qw, sc, ze, c, shape in ws]
+        mm = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            for x, w in zip(xs, wf):
+                torch.nn.functional.linear(x.float(), w)
+            mm.append(time.perf_counter() - t0)
+        st, sm = summarize(samples), summarize(mm)
+        return {"config": name, "M": m, "threads": torch.get_num_threads(), "warmups": warm, "reps": reps,
+                "layers_scaled": layers, "bytes": nbytes,
+                "us_median": st["median"] * 1e6, "us_p25": st["p25"] * 1e6, "us_p75": st["p75"] * 1e6,
+                "matmul_only_us_median": sm["median"] * 1e6, "gbs": nbytes / st["median"] / 1e9,
+                "s_per_step_scaled": st["median"] * layers if layers else None}
+
+    threads = torch.get_num_threads()
+    rows = [row("C1", [singles["C1"]], 1, None, 20, 3), row("C2", [singles["C2"]], 1, None, 20, 3),
+            row("C2", [singles["C2"]], 4, None, 20, 3), row("C3", [singles["C3"]], 1, None, 20, 3),
+            row("C4 (one layer of 32)", [c4_layer[n] for n, _, _ in PROJS], 1, LAYERS, 20, 3),
+            row("C5 (one layer of 80, lm_head excluded)", list(c5_layer.values()), 1, C5_LAYERS, 3, 1)]
+    torch.set_num_threads(1)
     try:
-        text = open(TRAFFIC_PROFILE).read()
-        rec = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
-    except (OSError, IndexError, ValueError):
-        return None
-    return rec["traffic_bytes_per_launch"] if rec.get("kernel") == kernel else None
+        rows.append(row("C1", [singles["C1"]], 1, None, 10, 3))
+    finally:
+        torch.set_num_threads(threads)
+    c4 = rows[4]
+    return {"value": c4["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"one Llama-3-8B layer (7 linears, {c4['bytes'] / 1e6:.1f} MB packed INT4 g128 asym, M=1) "
+                       f"of the benchmark stack, unpack -> dequantize -> fp32 F.linear (oracle/cpu_path.py), "
+                       f"median of {c4['reps']} after 3 warm-ups; rows for C1-C5 and a 1-thread C1 row"),
+            "us_per_layer": c4["us_median"], "matmul_only_us_per_layer": c4["matmul_only_us_median"],
+            "os_cpu_count": os.cpu_count(), "rows": rows}
 
 
+# ------------------------------------------------------------------- main
 def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "the sharding design is described in DESIGN.md", file=sys.stderr)
+              "DESIGN.md describes how the path would shard", file=sys.stderr)
         return 2
     import torch
 
@@ -510,6 +616,7 @@ def main():
     eng = Engine(torch)
     torch.backends.cuda.matmul.allow_tf32 = False
     log(f"device: {torch.cuda.get_device_name(0)}  torch {torch.__version__}")
+    extra = not args.no_extra
 
     if args.calibrate_copy:
         src = torch.empty(2 ** 28, dtype=torch.int32, device="cuda").fill_(1)
@@ -520,150 +627,218 @@ def main():
         log("calibration copy: 1 GiB read + 1 GiB write, 3 times")
         del src, dst
 
+    # ---- 1. build every input of the timed legs (resident until the end)
     t0 = time.perf_counter()
     cfg, stack, xs = build_stack(torch, args.layers)
+    ceiling_buf = torch.empty(CEILING_BYTES // 4, dtype=torch.int32, device="cuda").random_()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    if extra:
+        other = {key: build_stack(torch, args.layers, seed=20251202, cfg=c)
+                 for key, c in (("INT8 per-channel sym", QuantConfig(8, None, True)),
+                                ("INT2 g64 asym", QuantConfig(2, 64, False)))}
+        bgen = torch.Generator(device="cuda").manual_seed(20251203)
+        batch_xs = {m: make_xs(torch, args.layers, m, bgen) for m in (2, 4, 8)}
+        pgen = torch.Generator(device="cuda").manual_seed(20251205)
+        gamma = torch.rand(HIDDEN, generator=pgen, device="cuda", dtype=torch.float16) + 0.5
+        ups = [torch.randn(1, INTER, generator=pgen, device="cuda", dtype=torch.float16) for _ in stack]
+        c5 = c5_build(torch)
+        singles = {name: single_copies(torch, n, k, QuantConfig(*spec), seed=n * 7 + k, outliers=name == "C3")
+                   for name, n, k, spec, _ in SINGLE_CONFIGS if name != "C2_M4"}
+        sgen = torch.Generator(device="cuda").manual_seed(20251208)
+        single_x = {name: torch.randn(m, k, generator=sgen, device="cuda", dtype=torch.float16)
+                    for name, n, k, _, m in SINGLE_CONFIGS}
     torch.cuda.synchronize()
-    log(f"built {args.layers}-layer INT4 stack in {time.perf_counter() - t0:.1f}s")
+    build_s = time.perf_counter() - t0
+    log(f"built every input in {build_s:.1f}s")
 
-    modes = {}
-    want = [m.strip() for m in args.modes.split(",") if m.strip()]
-    if "stack" not in want:
-        want.insert(0, "stack")
-    for mode in want:
-        launches, step_bytes, ms, per = run_mode(torch, eng, stack, xs, mode, args.steps, args.warmup)
-        st = summarize(per)
-        inst = kernel_instances(eng, launches)
-        modes[mode] = {"launches_per_step": len(launches), "bytes_per_step": step_bytes, "ms_per_step": ms,
-                       "step_ms": st, "gbs": step_bytes / (ms * 1e-3) / 1e9,
-                       "us_per_layer": ms * 1e3 / args.layers,
-                       "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
-                       "kernel_instances": {k: len(v) for k, v in inst.items()}}
-        log(f"mode {mode}: {ms:.3f} ms/step  {modes[mode]['gbs']:.1f} GB/s  "
-            f"{modes[mode]['us_per_layer']:.2f} us/layer  ({len(launches)} launches)")
-        if mode == "stack":
-            head_launches, head_bytes, head_ms, head_inst = launches, step_bytes, ms, inst
+    # ---- 2. capture every graph (host only)
+    modes = [m.strip() for m in args.modes.split(",") if m.strip()]
+    if "stack" not in modes:
+        modes.insert(0, "stack")
+    c4_launches = {mode: step_launches(stack, xs, mode) for mode in modes}
+    legs = {f"C4 {mode}": gemv_leg(torch, eng, mode, c4_launches[mode], args.steps, args.warmup, args.layers)
+            for mode in modes}
+    singles_meta = {}
+    if extra:
+        from dequant_project_amd import fused
 
-    # the stack step runs a single kernel instance: its mean launch duration is
-    # the timed region over the launches in it (gaps between the 14 long
-    # launches are included, a few percent)
-    dominant = max(head_inst, key=lambda k: sum(head_inst[k]))
-    n_dom = len(head_inst[dominant])
-    bytes_per_launch = sum(head_inst[dominant]) / n_dom
-    mean_us = head_ms * 1e3 / len(head_launches) if len(head_inst) == 1 else None
-    achieved = bytes_per_launch / (mean_us * 1e-6) / 1e9 if mean_us else None
-    if mean_us:
-        log(f"dominant kernel {dominant}: {n_dom} launches/step, {bytes_per_launch / 1e6:.1f} MB/launch, "
-            f"{mean_us:.2f} us/launch, {achieved:.1f} GB/s")
-    else:
-        log(f"dominant kernel {dominant}: {n_dom} launches/step, {bytes_per_launch / 1e6:.1f} MB/launch "
-            f"(the step mixes {len(head_inst)} kernel instances: no per-launch duration)")
-    traffic = profiled_traffic(dominant)
-    roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / PEAK_GBS if achieved else None,
-                "traffic": traffic, "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
-                                                    "copy-calibrated; profiles/)", "kernel": dominant,
-                "bytes_per_launch": bytes_per_launch, "mean_launch_us": mean_us, "launches_per_step": n_dom}
+        for key, (_, ostack, oxs) in other.items():
+            legs[f"stack {key}"] = gemv_leg(torch, eng, key, step_launches(ostack, oxs, "stack"), args.steps,
+                                            args.warmup, args.layers)
+        for m, mxs in batch_xs.items():
+            legs[f"stack M={m}"] = gemv_leg(torch, eng, f"M={m}", step_launches(stack, mxs, "stack"), args.steps,
+                                            args.warmup, args.layers)
+        legs["prologue plain"] = gemv_leg(torch, eng, "plain", step_launches(stack, xs, "decode"), args.steps,
+                                          args.warmup, args.layers)
 
-    # the same stack step in the other formats (sustained bandwidth of the
-    # INT8 and INT2 kernels over the Llama-3-8B shapes)
-    other_stacks = {}
-    if not args.no_extra:
-        for key, ocfg in [("INT8 per-channel sym", QuantConfig(8, None, True)),
-                          ("INT2 g64 asym", QuantConfig(2, 64, False))]:
-            _, ostack, oxs = build_stack(torch, args.layers, seed=20251202, cfg=ocfg)
-            torch.cuda.synchronize()
-            launches, step_bytes, ms, per = run_mode(torch, eng, ostack, oxs, "stack", args.steps, args.warmup)
-            inst = kernel_instances(eng, launches)
-            other_stacks[key] = {"launches_per_step": len(launches), "bytes_per_step": step_bytes,
-                                 "ms_per_step": ms, "step_ms": summarize(per),
-                                 "gbs": step_bytes / (ms * 1e-3) / 1e9, "us_per_layer": ms * 1e3 / args.layers,
-                                 "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
-                                 "kernel_instances": {k: len(v) for k, v in inst.items()}}
-            log(f"stack {key}: {ms:.3f} ms/step  {other_stacks[key]['gbs']:.1f} GB/s  "
-                f"{other_stacks[key]['us_per_layer']:.2f} us/layer  ({len(launches)} launches)")
-            del ostack, oxs, launches
-            torch.cuda.empty_cache()
+        def run_fused():
+            for li, (layer, x) in enumerate(zip(stack, xs)):
+                fused.gemv_rmsnorm(x["qkv"], gamma, 1e-5, [layer["q_proj"], layer["k_proj"], layer["v_proj"]])
+                eng.gemv_group([x["o"]], [layer["o_proj"]])
+                fused.gemv_rmsnorm(x["gate_up"], gamma, 1e-5, [layer["gate_proj"], layer["up_proj"]])
+                fused.gemv_swiglu(x["down"], ups[li], layer["down_proj"])
 
-    # the same INT4 stack at the other batch sizes the benchmark configs name
-    # (C4: M in {1, 2, 4, 8})
-    batch_stacks = {}
-    if not args.no_extra:
-        gen = torch.Generator(device="cuda").manual_seed(20251203)
-        for m in (2, 4, 8):
-            mxs = make_xs(torch, args.layers, m, gen)
-            launches, step_bytes, ms, per = run_mode(torch, eng, stack, mxs, "stack", args.steps, args.warmup)
-            inst = kernel_instances(eng, launches)
-            batch_stacks[f"M={m}"] = {"launches_per_step": len(launches), "bytes_per_step": step_bytes,
-                                      "ms_per_step": ms, "step_ms": summarize(per),
-                                      "gbs": step_bytes / (ms * 1e-3) / 1e9, "us_per_layer": ms * 1e3 / args.layers,
-                                      "pct_peak": 100 * step_bytes / (ms * 1e-3) / 1e9 / PEAK_GBS,
-                                      "kernel_instances": {k: len(v) for k, v in inst.items()}}
-            log(f"stack INT4 M={m}: {ms:.3f} ms/step  {batch_stacks[f'M={m}']['gbs']:.1f} GB/s  "
-                f"{batch_stacks[f'M={m}']['us_per_layer']:.2f} us/layer")
-            del mxs, launches
+        legs["prologue fused"] = Leg(torch, "fused", capture(torch, run_fused), args.steps, args.warmup,
+                                     legs["prologue plain"].step_bytes, layers=args.layers)
+        for mode, ls in c5_launches(*c5).items():
+            legs[f"C5 {mode}"] = gemv_leg(torch, eng, mode, ls, args.steps, args.warmup, C5_LAYERS)
+        for name, n, k, spec, m in SINGLE_CONFIGS:
+            pws = singles["C2" if name == "C2_M4" else name]
+            x = single_x[name]
 
-    # the fused small GEMM over the stack (M > 8: the reference's dequantize +
-    # F.linear path) and the decode launches with fused prologues
-    gemm = {}
-    prologue = None
-    if not args.no_extra:
+            def fn(pws=pws, x=x):
+                for p in pws:
+                    eng.gemv_group([x], [p])
+
+            legs[f"single {name}"] = Leg(torch, name, capture(torch, fn), 10, 2)
+            singles_meta[name] = (n, k, spec, m, len(pws), launch_bytes([x], [pws[0]]),
+                                  eng.kernel_name([x], [pws[0]])[0])
+
+    def ceiling_fn():
+        eng.stream_read(ceiling_buf, sink)
+
+    ceiling = Leg(torch, "read ceiling", capture(torch, ceiling_fn), CEILING_REPS, CEILING_WARM,
+                  ceiling_buf.numel() * 4)
+
+    def empty_fn():
+        for _ in range(EMPTY_LAUNCHES):
+            eng.empty_kernel()
+
+    empty = Leg(torch, "empty kernels", capture(torch, empty_fn), 10, 3)
+    torch.cuda.synchronize()
+    log(f"captured {len(legs) + 2} graphs")
+
+    # ---- 3. timed legs, back to back, one synchronization at the end
+    ceiling.enqueue()
+    for leg in legs.values():
+        leg.enqueue()
+    empty.enqueue()
+    torch.cuda.synchronize()
+
+    results = {key: leg.result() for key, leg in legs.items()}
+    ceil_r = ceiling.result()
+    ceil_gbs = ceiling.step_bytes / (ceil_r["step_ms"]["median"] * 1e-3) / 1e9
+    empty_r = empty.result()
+    ceilings = {"stream_read_gbs": ceil_gbs, "stream_read_pct_peak": 100 * ceil_gbs / PEAK_GBS,
+                "stream_read_bytes": ceiling.step_bytes, "stream_read_reps": CEILING_REPS,
+                "stream_read_step_ms": ceil_r["step_ms"],
+                "stream_read_kernel": "stream_read_kernel (dq_stream_read: non-temporal, 1 KiB per wave and load)",
+                "empty_kernel_us_per_launch": empty_r["step_ms"]["median"] * 1e3 / EMPTY_LAUNCHES,
+                "empty_kernel_launches_per_graph": EMPTY_LAUNCHES}
+    log(f"read ceiling {ceil_gbs:.0f} GB/s ({100 * ceil_gbs / PEAK_GBS:.1f}%), empty kernel "
+        f"{ceilings['empty_kernel_us_per_launch']:.2f} us per launch in a graph")
+    for mode in modes:
+        r = results[f"C4 {mode}"]
+        log(f"mode {mode}: {r['ms_per_step']:.3f} ms/step  {r['gbs']:.1f} GB/s  {r['us_per_layer']:.2f} us/layer  "
+            f"({r['launches_per_step']} launches)")
+
+    # ---- 4. kernel durations of the headline's launches (launch-event hook)
+    launches = c4_launches["stack"]
+    durs = kernel_durations(torch, eng, launches, args.steps)
+    names = [eng.kernel_name(x, p)[0] for _, x, p in launches]
+    per_name = {}
+    for i, nm in enumerate(names):
+        per_name.setdefault(nm, []).append(i)
+    dominant = max(per_name, key=lambda nm: sum(launch_bytes(launches[i][1], launches[i][2]) for i in per_name[nm]))
+    dom_idx = per_name[dominant]
+    dom_bytes = sum(launch_bytes(launches[i][1], launches[i][2]) for i in dom_idx) / len(dom_idx)
+    dom_us = statistics.mean(d[i] for d in durs for i in dom_idx)
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    kernel_sum_us = statistics.mean(sum(d) for d in durs)
+    gap_us = (results["C4 stack"]["ms_per_step"] * 1e3 - kernel_sum_us) / len(launches)
+    traffic, trec = profiled_traffic(dominant)
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s", "frac": achieved / PEAK_GBS,
+                "traffic": traffic, "kernel": dominant, "bytes_per_launch": dom_bytes, "mean_launch_us": dom_us,
+                "launches_per_step": len(dom_idx),
+                "method": (f"algorithmic bytes per launch / mean kernel duration over {args.steps} eager passes of "
+                           "the headline step's launches, each bracketed by hipExtLaunchKernelGGL start/stop events "
+                           "on its launch stream (dq_set_launch_events), run right after the timed replays"),
+                "kernel_time_per_step_us": kernel_sum_us, "launch_gap_us": gap_us,
+                "traffic_unit": "bytes per launch",
+                "traffic_source": ("static: rocprofv3 FETCH_SIZE + WRITE_SIZE of this kernel on this workload, "
+                                   "copy-calibrated, profiles/" + os.path.basename(TRAFFIC_PROFILE)
+                                   if traffic else "no committed counter summary for this kernel")}
+    if trec:
+        roofline["traffic_vs_algorithmic"] = traffic / trec["algorithmic_bytes_per_launch"]
+    log(f"dominant kernel {dominant}: {len(dom_idx)} launches/step, {dom_bytes / 1e6:.1f} MB/launch, "
+        f"{dom_us:.2f} us/launch kernel time, {achieved:.1f} GB/s ({100 * achieved / PEAK_GBS:.1f}%); "
+        f"launch gap {gap_us:.2f} us")
+
+    other_stacks, batch_stacks, prologue, c5_r, single_r = {}, {}, None, None, {}
+    if extra:
+        for key in other:
+            r = other_stacks[key] = results[f"stack {key}"]
+            log(f"stack {key}: {r['ms_per_step']:.3f} ms/step  {r['gbs']:.1f} GB/s  {r['us_per_layer']:.2f} us/layer")
+        for m in batch_xs:
+            r = batch_stacks[f"M={m}"] = results[f"stack M={m}"]
+            log(f"stack INT4 M={m}: {r['ms_per_step']:.3f} ms/step  {r['gbs']:.1f} GB/s  "
+                f"{r['us_per_layer']:.2f} us/layer")
+        prologue = {"plain": results["prologue plain"], "fused_prologues": results["prologue fused"],
+                    "bytes_per_step": legs["prologue plain"].step_bytes}
+        log(f"decode launches: plain {prologue['plain']['us_per_layer']:.2f} us/layer, with fused prologues "
+            f"{prologue['fused_prologues']['us_per_layer']:.2f} us/layer")
+        c5_r = {"layers": C5_LAYERS, "stack": results["C5 stack"], "decode": results["C5 decode"]}
+        log(f"C5: stack {c5_r['stack']['ms_per_step']:.3f} ms/step {c5_r['stack']['gbs']:.1f} GB/s "
+            f"{c5_r['stack']['us_per_layer']:.2f} us/layer; decode {c5_r['decode']['ms_per_step']:.3f} ms/step "
+            f"{c5_r['decode']['gbs']:.1f} GB/s")
+        for name, (n, k, spec, m, copies, b, kern) in singles_meta.items():
+            st = results[f"single {name}"]["step_ms"]
+            us = st["median"] * 1e3 / copies
+            single_r[name] = {"shape": [n, k], "M": m, "format": f"INT{spec[0]} g{spec[1] or 'pc'} "
+                              f"{'sym' if spec[2] else 'asym'}", "copies": copies, "bytes_per_call": b,
+                              "us_per_call": us, "us_p25": st["p25"] * 1e3 / copies, "us_p75": st["p75"] * 1e3 / copies,
+                              "gbs": b / (us * 1e-6) / 1e9, "pct_peak": 100 * b / (us * 1e-6) / 1e9 / PEAK_GBS,
+                              "kernel": kern}
+            log(f"{name}: {us:.2f} us/call ({single_r[name]['gbs']:.0f} GB/s) in a graph of {copies} copies")
+
+    # ---- 5. legs that build and time in place (their builds reuse cached memory)
+    gemm, axis = {}, []
+    if extra:
         for m in (16, 64):
-            gemm[f"M={m}"] = gemm_stack(torch, stack, m, args.steps, args.warmup // 4)
-            g = gemm[f"M={m}"]
+            g = gemm[f"M={m}"] = gemm_stack(torch, stack, m, args.steps, args.warmup)
             log(f"gemm_small stack M={m}: {g['ms_per_step']:.3f} ms/step  {g['gbs']:.1f} GB/s  "
                 f"(dequantize + F.linear {g['dequantize_plus_linear_ms_per_step']:.3f} ms/step, "
                 f"{g['speedup_vs_dequantize_plus_linear']:.2f}x)")
-        prologue = prologue_decode(torch, eng, stack, xs, args.steps, args.warmup)
-        log(f"decode launches: plain {prologue['plain']['us_per_layer']:.2f} us/layer, with fused prologues "
-            f"{prologue['fused_prologues']['us_per_layer']:.2f} us/layer")
+        axis = format_axis(torch, eng, args.steps, args.warmup)
+        for r in axis:
+            log(f"  {r['shape']:<13}{r['format']:<21}{r['us_median']:8.2f} us {r['gbs']:8.0f} GB/s "
+                f"{r['pct_peak']:5.1f}%  {r['speedup_vs_fp16']:5.2f}x vs fp16")
 
-    c5 = None
-    if not args.no_extra:
-        c5 = c5_stack(torch, eng, args.steps, args.warmup // 4)
-        log(f"C5 (Llama-3-70B shapes, INT4 attention / INT2 MLP / INT8 lm_head, {c5['stack']['bytes_per_step'] / 1e9:.2f} GB,"
-            f" built in {c5['build_s']:.0f}s): stack {c5['stack']['ms_per_step']:.3f} ms/step "
-            f"{c5['stack']['gbs']:.1f} GB/s {c5['stack']['us_per_layer']:.2f} us/layer; decode "
-            f"{c5['decode']['ms_per_step']:.3f} ms/step {c5['decode']['gbs']:.1f} GB/s")
-
-    extra = {}
-    if not args.no_extra:
-        for name, n, k, c, m in [("C1", 4096, 4096, QuantConfig(4, 128, False), 1),
-                                 ("C2", 11008, 4096, QuantConfig(8, None, True), 1),
-                                 ("C2_M4", 11008, 4096, QuantConfig(8, None, True), 4),
-                                 ("C3", 4096, 11008, QuantConfig(2, 64, False), 1)]:
-            key, res = single_config(torch, eng, name, n, k, c, m)
-            extra[key] = res
-            log(f"{key}: {res['us_per_call']:.2f} us/call ({res['gbs']:.0f} GB/s) in a graph of "
-                f"{res['copies']} distinct copies")
-
+    # ---- 6. CPU baseline (needs the extra legs' single-config weights)
     cpu = None
-    if not args.no_cpu_baseline:
+    if extra and not args.no_cpu_baseline:
         t0 = time.perf_counter()
-        cpu = cpu_baseline(torch, stack)
+        cpu = cpu_baseline(torch, stack[0], {k: singles[k][0] for k in ("C1", "C2", "C3")}, c5[0][0])
         log(f"cpu baseline: {cpu['value']:.3f} GB/s on {cpu['cores']} threads ({time.perf_counter() - t0:.1f}s)")
 
-    gbs = head_bytes / (head_ms * 1e-3) / 1e9
+    head_r = results["C4 stack"]
+    gbs = head_r["gbs"]
     line = {
         "metric": METRIC, "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": head_ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "ms_per_step": head_r["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int4 codes -> fp16 (q-z), fp16 x fp16 products, fp32 accumulate",
         "data": "synthetic (seeded fp16 N(0,0.02) weights quantized on the GPU; fp16 N(0,1) activations)",
         "config": {"workload": "C4: Llama-3-8B decoder linear set (32 layers x q,k,v,o,gate,up,down), "
                                "INT4 g128 asym, M=1",
-                   "layers": args.layers, "batch": 1, "bytes_per_step": head_bytes,
-                   "launches_per_step": len(head_launches),
+                   "layers": args.layers, "batch": 1, "bytes_per_step": head_r["bytes_per_step"],
+                   "launches_per_step": head_r["launches_per_step"],
                    "grouping": "stack: launches of up to 16 independent GEMVs of equal K"},
         "pct_of_peak": 100 * gbs / PEAK_GBS,
-        "us_per_layer": head_ms * 1e3 / args.layers,
+        "us_per_layer": head_r["us_per_layer"],
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "modes": modes,
+        "ceilings": ceilings,
+        "protocol": {"build_s": build_s, "order": ["read ceiling"] + list(legs) + ["empty kernels"],
+                     "note": "every input built and every graph captured before timing; nothing freed; the legs "
+                             "replayed back to back with one synchronization at the end"},
+        "modes": {mode: results[f"C4 {mode}"] for mode in modes},
         "other_format_stacks": other_stacks,
         "batch_stacks": batch_stacks,
         "gemm_small_stacks": gemm,
         "decode_with_fused_prologues": prologue,
-        "c5_llama3_70b_stack": c5,
-        "single_configs": extra,
+        "c5_llama3_70b_stack": c5_r,
+        "single_configs": single_r,
+        "format_axis": axis,
     }
     print(json.dumps(line, default=lambda o: sorted(o) if isinstance(o, set) else str(o)), flush=True)
     return 0

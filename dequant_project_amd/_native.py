@@ -96,6 +96,8 @@ SIGNATURES = {
     "dq_dequantize": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P]),
     "dq_unpack": (_I, [_P, _P, _I64, _I64, _I64, _I, _P]),
     "dq_add_one": (_I, [_P, _P, _I64, _P]),
+    "dq_stream_read": (_I, [_P, _I64, _P, _P]),
+    "dq_empty_kernel": (_I, [_P]),
 }
 
 

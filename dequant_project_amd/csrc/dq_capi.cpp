@@ -458,6 +458,21 @@ int dq_unpack(const uint32_t* qweight, int32_t* out, int64_t N, int64_t K, int64
                                          reinterpret_cast<hipStream_t>(stream)));
 }
 
+int dq_stream_read(const void* data, int64_t bytes, uint32_t* sink, dq_stream_t stream) {
+  g_error.clear();
+  if (bytes < 0 || bytes % 16 != 0)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("bytes must be a non-negative multiple of 16, got ", bytes));
+  if (bytes == 0) return DQ_OK;
+  if (!data || !sink) return fail(DQ_ERR_INVALID_ARGUMENT, "data and sink must not be NULL");
+  if (!aligned16(data)) return fail(DQ_ERR_INVALID_ARGUMENT, "data must be 16-byte aligned");
+  return launch_status(dq::launch_stream_read(data, bytes, sink, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dq_empty_kernel(dq_stream_t stream) {
+  g_error.clear();
+  return launch_status(dq::launch_empty(reinterpret_cast<hipStream_t>(stream)));
+}
+
 int dq_add_one(const float* in, float* out, int64_t n, dq_stream_t stream) {
   g_error.clear();
   if (n < 0) return fail(DQ_ERR_INVALID_ARGUMENT, cat("n must be non-negative, got ", n));

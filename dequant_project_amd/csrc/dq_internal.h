@@ -30,10 +30,10 @@ void set_launch_events(hipEvent_t start, hipEvent_t stop);
 
 // Launch geometry a grouped GEMV would use: waves per tile along K for each
 // problem (wk[0..count-1]), the launch's rows per tile, and which kernel runs:
-// *mfma == 0: gemv_kernel<bits, sym, inter, MT, rows, 1> (VALU dot products, M > 1);
-// *mfma == 1: gemv_mfma_kernel<bits, sym, inter, rows / 16> (2 <= M <= 8);
+// *mfma == 1: gemv_quad_kernel<bits, sym, inter, rows / 4, MG> (2 <= M <= 8);
 // *mfma == 2: gemv_m1_kernel<bits, sym, inter, rows, false> (M = 1, VALU dots);
-// *mfma == 3: gemv_m1_kernel<bits, sym, inter, rows, true> (M = 1, MFMA dots).
+// *mfma == 3: gemv_m1_kernel<bits, sym, inter, rows, true> (M = 1, MFMA dots);
+// *mfma == 4: gemv_m1_pipe_kernel<bits, sym, inter, rows> (M = 1, pipelined walk).
 void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows, int* mfma);
 
 // All problems of one launch share M and the format (bits, symmetry, layout).
@@ -75,5 +75,10 @@ hipError_t launch_dequantize(const DequantProblem& p, hipStream_t stream);
 hipError_t launch_unpack(const uint32_t* qweight, int32_t* out, int64_t N, int64_t K, int bits,
                          bool interleaved, hipStream_t stream);
 hipError_t launch_add_one(const float* in, float* out, int64_t n, hipStream_t stream);
+
+// Measurement kernels: a streaming read of `bytes` (a multiple of 16) and an
+// empty kernel (one wave).
+hipError_t launch_stream_read(const void* data, int64_t bytes, uint32_t* sink, hipStream_t stream);
+hipError_t launch_empty(hipStream_t stream);
 
 }  // namespace dq

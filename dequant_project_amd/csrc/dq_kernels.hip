@@ -271,7 +271,7 @@ struct TilePos {
   int row0;     // first row of this wave's tile
   int cb, ce;   // chunk range [cb, ce) of this wave (its share of K)
   int kw, wk;   // this wave's share index and the number of shares
-  bool active;  // the block-tile has a tile for this wave
+  int active;   // the block-tile has a tile for this wave (an int: a struct copy then carries no padding bytes)
 };
 
 // `p` is the problem of the previous block-tile of this block (block-tiles
@@ -930,6 +930,225 @@ gemv_m1_kernel(const KernelBatch b) {
     } else {
       bt += gridDim.x;
     }
+  }
+}
+
+// ------------------------------------- gemv, M = 1, software-pipelined walk
+// The M = 1 kernel above issues a batch's loads, then computes it: while a
+// wave does its math it has no load in flight, so the bytes in flight per CU
+// (what sets the achieved bandwidth once HBM latency is queue-bound) fall
+// with the VALU time. This kernel keeps a batch in flight at all times with
+// the same registers: row r of the next batch (which may belong to the next
+// tile of the wave's walk, or to another problem) is issued as soon as row r
+// of the current batch has been computed.
+//
+// Activations: the block stages each batch's 64 chunk columns once in LDS,
+// already in pair order (thread t forms the pairs of word t % 4 of column
+// t / 4), double-buffered, one LDS-only barrier per batch (the weight loads
+// stay in flight across it). A wave reads its pairs with ds_read_b128 when a
+// batch starts, so the next batch's activations need no second set of
+// registers while the current batch's math runs (that set would drop the
+// kernel to four waves per SIMD), and the pairs are formed once per block
+// instead of once per wave.
+//
+// Launches whose tiles are one wave wide (wk = 1): the four waves of a block
+// then walk the same batches of the same block-tiles (block-tiles never mix
+// problems), so every wave meets every barrier; a wave whose slot of a
+// block-tile is empty walks its batches with out-of-range loads and stores
+// nothing.
+
+// Load addressing of one batch: descriptors and row offsets are wave-uniform
+// (SGPRs), the chunk-column offsets per lane. Rows of an empty slot and every
+// load of a batch past the walk's end get out-of-range offsets: they return
+// zeros and read nothing.
+template <int R>
+struct BatchAddr {
+  __amdgpu_buffer_rsrc_t wbuf, sbuf, zbuf;
+  uint32_t woff, moff;
+  uint32_t wrow[R], mrow[R];
+};
+
+template <int BITS, bool SYM, int R>
+__device__ __forceinline__ void batch_addr(const KernelProblem& d, int row0, int cbase, int ce, int lane, bool live,
+                                           BatchAddr<R>& a) {
+  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+  const uint32_t meta_row_bytes = static_cast<uint32_t>(d.n_groups) * 2;
+  a.wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+  a.sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row_bytes);
+  a.zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row_bytes);
+  const int c = cbase + lane;
+  const bool in = live && c < min(ce, cbase + 64);
+  a.woff = in ? static_cast<uint32_t>(c) * 16u : kOutOfRange;
+  a.moff = in ? group_of(d, c) * 2u : kOutOfRange;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t row = static_cast<uint32_t>(min(row0 + r, d.N - 1));  // past N: re-read N-1
+    a.wrow[r] = row * row_bytes;
+    a.mrow[r] = row * meta_row_bytes;
+  }
+}
+
+template <bool SYM, int R>
+__device__ __forceinline__ void issue_row(const BatchAddr<R>& a, int r, uint32_t& z, uint32_t& s, u32x4& w) {
+  if constexpr (!SYM) z = __builtin_amdgcn_raw_buffer_load_b16(a.zbuf, a.moff, a.mrow[r], 0);
+  s = __builtin_amdgcn_raw_buffer_load_b16(a.sbuf, a.moff, a.mrow[r], 0);
+  w = __builtin_amdgcn_raw_buffer_load_b128(a.wbuf, a.woff, a.wrow[r], 2);
+}
+
+// One batch's activations in LDS, in pair order: chunk column c at
+// c * kStride (a 16-byte pad per column spreads a wave's reads over the
+// banks); thread t of the block forms word t % 4 of column t / 4.
+template <int BITS>
+struct PairStage {
+  using F = Fmt<BITS>;
+  static constexpr int kWordBytes = F::PER * 2;        // one word's activations (= its pairs)
+  static constexpr int kColumnBytes = F::CPL * 2;      // 4 words
+  static constexpr int kStride = kColumnBytes + 16;
+  static constexpr int kBufBytes = 64 * kStride;
+  static constexpr int kWordDwords = kWordBytes / 4;   // PER / 2
+};
+
+// Thread t's word of the batch starting at column cbase (columns >= ce and a
+// batch past the walk's end load zeros).
+template <int BITS>
+__device__ __forceinline__ void pair_stage_issue(const KernelProblem& d, int cbase, int ce, bool live,
+                                                 uint32_t (&raw)[PairStage<BITS>::kWordDwords]) {
+  using PS = PairStage<BITS>;
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(d.K) * 2u);
+  const int t = static_cast<int>(threadIdx.x);
+  const int c = cbase + (t >> 2);
+  const uint32_t off = live && c < ce ? static_cast<uint32_t>(c) * PS::kColumnBytes + (t & 3) * PS::kWordBytes
+                                      : kOutOfRange;
+  if constexpr (PS::kWordDwords == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(xbuf, off, 0, 0);
+    raw[0] = v[0];
+    raw[1] = v[1];
+  } else {
+#pragma unroll
+    for (int q = 0; q < PS::kWordDwords / 4; ++q) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xbuf, off + 16u * q, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) raw[4 * q + e] = v[e];
+    }
+  }
+}
+
+template <int BITS, bool INTER>
+__device__ __forceinline__ void pair_stage_write(unsigned char* buf, const uint32_t (&raw)[PairStage<BITS>::kWordDwords]) {
+  using PS = PairStage<BITS>;
+  h2 xp[Fmt<BITS>::PAIRS];
+  x_pairs_from_dwords<BITS, INTER>(raw, xp);
+  const int t = static_cast<int>(threadIdx.x);
+  unsigned char* dst = buf + (t >> 2) * PS::kStride + (t & 3) * PS::kWordBytes;
+  if constexpr (PS::kWordDwords == 2) {
+    *reinterpret_cast<u32x2*>(dst) = u32x2{__builtin_bit_cast(uint32_t, xp[0]), __builtin_bit_cast(uint32_t, xp[1])};
+  } else {
+#pragma unroll
+    for (int q = 0; q < PS::kWordDwords / 4; ++q) {
+      u32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(uint32_t, xp[4 * q + e]);
+      *reinterpret_cast<u32x4*>(dst + 16 * q) = v;
+    }
+  }
+}
+
+template <int BITS>
+__device__ __forceinline__ void pair_stage_read(const unsigned char* buf, int lane, h2 (&xr)[4][Fmt<BITS>::PAIRS]) {
+  using F = Fmt<BITS>;
+  using PS = PairStage<BITS>;
+  const unsigned char* src = buf + lane * PS::kStride;
+#pragma unroll
+  for (int k = 0; k < PS::kColumnBytes / 16; ++k) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xr[(4 * k + e) / F::PAIRS][(4 * k + e) % F::PAIRS] = as_h2(v[e]);
+  }
+}
+
+template <int BITS, bool SYM, bool INTER, int R>
+__global__ void __launch_bounds__(kGemvThreads)
+gemv_m1_pipe_kernel(const KernelBatch b) {
+  using F = Fmt<BITS>;
+  using PS = PairStage<BITS>;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  __shared__ __align__(16) unsigned char xs[2 * PS::kBufBytes];
+  ClassMagics<BITS> cm;
+  cm.init();
+  const int total = b.bt_start[b.count];
+  int p = 0;
+  int bt = static_cast<int>(blockIdx.x);
+  if (bt >= total) return;  // block-uniform: the whole block leaves
+  TilePos t = locate(b, bt, wave, R, p);
+  int cb = t.cb;
+  int par = 0;
+  BatchAddr<R> a;
+  uint32_t raw[PS::kWordDwords];
+  uint32_t z[R], s[R];
+  u32x4 w[R];
+  // the first batch: activations staged, rows in flight
+  pair_stage_issue<BITS>(b.p[t.p], cb, t.ce, true, raw);
+  batch_addr<BITS, SYM, R>(b.p[t.p], t.row0, cb, t.ce, lane, t.active, a);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    issue_row<SYM, R>(a, r, z[r], s[r], w[r]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  pair_stage_write<BITS, INTER>(xs, raw);
+  lds_barrier();
+  float yacc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) yacc[r] = 0.f;
+  for (;;) {
+    // where the next batch is: the next 64 columns of this tile, or the
+    // first batch of the next block-tile (the same for the whole block)
+    int ncb = cb + 64;
+    int nbt = bt, np = p;
+    TilePos nt = t;
+    const bool tile_end = ncb >= t.ce;
+    if (tile_end) {
+      nbt = bt + static_cast<int>(gridDim.x);
+      if (nbt < total) {
+        nt = locate(b, nbt, wave, R, np);
+        ncb = nt.cb;
+      }
+    }
+    const bool nvalid = nbt < total;  // block-uniform
+    // the current batch's pairs and bias sums
+    h2 xr[4][F::PAIRS];
+    pair_stage_read<BITS>(xs + par * PS::kBufBytes, lane, xr);
+    float S, C;
+    bias_sums<BITS>(xr, S, C);
+    if constexpr (SYM) C = __builtin_fmaf(static_cast<float>(F::BIAS), S, C);
+    // the next batch's activations (issued first: vmcnt retires in order),
+    // then its rows as the current ones free their registers
+    pair_stage_issue<BITS>(b.p[np], ncb, nt.ce, nvalid, raw);
+    batch_addr<BITS, SYM, R>(b.p[np], nt.row0, ncb, nt.ce, lane, nvalid && nt.active, a);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float corr = SYM ? C : __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(z[r])), S, C);
+      const float v = biased_dot_m1<BITS, false>(w[r], xr, cm, lane) - corr;
+      yacc[r] = __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(s[r])), v, yacc[r]);
+      issue_row<SYM, R>(a, r, z[r], s[r], w[r]);  // row r of the next batch, into the freed registers
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (tile_end) {
+      wave_sum_rows<R>(yacc);
+      if (t.active && (lane & 15) == 15)
+        store_rows<R / 4>(b.p[t.p].y, t.row0 + (lane >> 4) * (R / 4), b.p[t.p].N, yacc);
+#pragma unroll
+      for (int r = 0; r < R; ++r) yacc[r] = 0.f;
+    }
+    if (!nvalid) break;
+    par ^= 1;
+    pair_stage_write<BITS, INTER>(xs + par * PS::kBufBytes, raw);
+    lds_barrier();  // the other buffer was read before the previous barrier
+    cb = ncb;
+    bt = nbt;
+    p = np;
+    t = nt;
   }
 }
 
@@ -1734,6 +1953,38 @@ add_one_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t n)
     out[i] = in[i] + 1.0f;
 }
 
+// --------------------------------------------------------------- measurement
+// The benchmark's denominators (no reference counterpart in the kernels; the
+// reference measures its read ceiling with torch ops,
+// scripts/bandwidth_by_dtype.py:85-106):
+//   stream_read_kernel  reads `n16` 16-byte elements once, 1 KiB per wave and
+//                       load, eight loads in flight per lane, non-temporal
+//                       (the GEMV weights' policy): the practical HBM read
+//                       ceiling of a plain streaming read;
+//   empty_kernel        does nothing: the per-launch gap of back-to-back
+//                       launches in a HIP graph.
+// The xor of everything read decides one store that a real buffer never
+// triggers, so the loads cannot be dropped.
+constexpr uint32_t kReadMagic = 0x9e3779b9u;
+
+__global__ void __launch_bounds__(256) stream_read_kernel(const u32x4* __restrict__ src, int64_t n16,
+                                                          uint32_t* __restrict__ sink) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (; i + 7 * stride < n16; i += 8 * stride) {
+    u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u];
+  }
+  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == kReadMagic && acc.x == kReadMagic) sink[0] = acc.y;
+}
+
+__global__ void empty_kernel() {}
+
 
 // ----------------------------------------------------------------- launchers
 namespace {
@@ -1909,6 +2160,16 @@ constexpr bool m1_keeps_x(int bits) { return bits == 2; }
 constexpr int kKeepRun = 3;
 constexpr int kKeepRounds = 2;
 
+// The software-pipelined M = 1 kernel (gemv_m1_pipe_kernel) for launches of
+// one-wave tiles (wk = 1 for every problem: no barrier in its walk), INT4 and
+// INT8; INT2 launches keep their activation staging / keeping variants.
+bool m1_pipelined(int bits, const int* wks, int count) {
+  if (bits == 2) return false;
+  for (int i = 0; i < count; ++i)
+    if (wks[i] != 1) return false;
+  return true;
+}
+
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
   int wks[kMaxBatch];
@@ -1931,6 +2192,12 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
     const int grid = resident_blocks<kernel>();
     kb.run = kKeepRun;
     if (keep && bts >= kKeepRounds * grid) return launch_kernel(kernel, grid, kb, stream);
+  }
+  if constexpr (PRO == kProNone) {
+    if (m1_pipelined(BITS, wks, count)) {
+      constexpr auto kernel = gemv_m1_pipe_kernel<BITS, SYM, INTER, R>;
+      return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+    }
   }
   constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, kXmLoad>;
   return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
@@ -2182,6 +2449,7 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
   *mfma = M == 1 ? (m1_uses_mfma(bits) ? 3 : 2) : 0;
   *rows = rows_per_tile(ops, count);
   waves_per_tile(ops, count, bits, *rows, wk);
+  if (M == 1 && m1_pipelined(bits, wk, count)) *mfma = 4;
 }
 
 void set_launch_events(hipEvent_t start, hipEvent_t stop) {
@@ -2231,6 +2499,18 @@ hipError_t launch_unpack(const uint32_t* qweight, int32_t* out, int64_t N, int64
     case (8 << 1 | 1): return launch_unpack_t<8, true>(qweight, out, N, K, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_stream_read(const void* data, int64_t bytes, uint32_t* sink, hipStream_t stream) {
+  const int grid = resident_blocks<stream_read_kernel>();
+  hipLaunchKernelGGL(stream_read_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4*>(data), bytes / 16,
+                     sink);
+  return hipGetLastError();
+}
+
+hipError_t launch_empty(hipStream_t stream) {
+  hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, stream);
+  return hipGetLastError();
 }
 
 hipError_t launch_add_one(const float* in, float* out, int64_t n, hipStream_t stream) {

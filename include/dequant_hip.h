@@ -211,7 +211,11 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
  *                      rows_per_tile, false> (M = 1; VALU dot products), or
  *   *kernel_kind == 3: gemv_m1_kernel<bits, symmetric, interleaved,
  *                      rows_per_tile, true> (M = 1; dot products on the
- *                      matrix cores; not chosen by the current geometry).
+ *                      matrix cores; not chosen by the current geometry),
+ *   *kernel_kind == 4: gemv_m1_pipe_kernel<bits, symmetric, interleaved,
+ *                      rows_per_tile> (M = 1, INT4 and INT8 launches whose
+ *                      tiles are all one wave wide: the next batch's loads
+ *                      are issued while the current batch is computed).
  * Large INT2 launches of one-wave tiles with K >= 8192 take the M = 1
  * kernel's variant that stages the activations per block in LDS, those of
  * 8-row one-batch tiles (K <= 4096) the variant that keeps each wave's
@@ -250,6 +254,22 @@ int dq_unpack(const uint32_t* qweight, int32_t* out, int64_t N, int64_t K, int64
 /* out[i] = in[i] + 1 for fp32, the toolchain smoke kernel
  * (kernels/smoke.cu:9-25). Kept for export-surface parity. */
 int dq_add_one(const float* in, float* out, int64_t n, dq_stream_t stream);
+
+/* Measurement kernels for the benchmark's denominators (no reference
+ * counterpart in the kernels; the reference measures its read ceiling with
+ * torch ops, scripts/bandwidth_by_dtype.py:85-106, and quotes it in
+ * hardware.md:71-100):
+ *   dq_stream_read   reads `bytes` (a multiple of 16; data 16-byte aligned)
+ *                    once, non-temporal, 1 KiB per wave and load: the
+ *                    practical HBM read ceiling. sink (>= 4 bytes of device
+ *                    memory) is written only for a data pattern that real
+ *                    buffers do not produce; it exists so the loads cannot
+ *                    be dropped;
+ *   dq_empty_kernel  one wave that does nothing: the launch gap of
+ *                    back-to-back launches (e.g. in a HIP graph).
+ * Both launch on `stream` and may be captured. */
+int dq_stream_read(const void* data, int64_t bytes, uint32_t* sink, dq_stream_t stream);
+int dq_empty_kernel(dq_stream_t stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

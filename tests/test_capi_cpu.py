@@ -208,17 +208,21 @@ def test_gemv_plan_geometry():
         assert st == 0, lib.dq_last_error()
         return list(wk), rows.value, kind.value
 
-    # M = 1: gemv_m1_kernel (kind 2; kind 3, its MFMA-dot variant, is not chosen). INT4: 32 codes per 16-byte column. Rows per tile: 8 for
+    # M = 1: gemv_m1_kernel (kind 2; kind 3, its MFMA-dot variant, is not chosen),
+    # or gemv_m1_pipe_kernel (kind 4) when every problem's tiles are one wave wide
+    # (INT4 and INT8). INT4: 32 codes per 16-byte column. Rows per tile: 8 for
     # launches with >= 6144 tiles of 8 rows, else 4. wk: smallest of 1, 2, 4 giving
     # the launch 6144 waves (INT4), capped so each wave keeps >= 40 columns.
     assert plan([(14336, 4096)]) == ([2], 4, 2)
-    assert plan([(14336, 4096)] * 2) == ([1, 1], 4, 2)          # gate | up: 7168 waves already
+    assert plan([(14336, 4096)] * 2) == ([1, 1], 4, 4)          # gate | up: 7168 waves already
     assert plan([(4096, 14336)]) == ([4], 4, 2)                 # 448 columns: 112 per wave
     assert plan([(4096, 4096)]) == ([2], 4, 2)                  # 128 columns: 4 waves would leave 32
     assert plan([(1024, 4096)]) == ([2], 4, 2)
     assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 2)
-    assert plan([(14336, 4096)] * 16) == ([1] * 16, 8, 2)       # a stack of projections: 8-row tiles
-    assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 2)
+    assert plan([(14336, 4096)] * 16) == ([1] * 16, 8, 4)       # a stack of projections: 8-row tiles
+    assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 4)
+    assert plan([(4096, 14336)] * 16, bits=8, gs=None) == ([1] * 16, 8, 4)
+    assert plan([(14336, 4096)] * 16, bits=2, gs=64) == ([1] * 16, 8, 2)  # INT2: its own activation variants
     assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 2)  # 172 columns of 64 codes, 43 per wave
     assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 2)  # INT8 wants 8192 waves
     # 2 <= M <= 8: gemv_quad_kernel (kind 1) for every format and group size;

@@ -664,6 +664,67 @@ def test_grouped_launch_over_several_rounds(torch_gpu, bits, gs, sym, n, k, coun
         assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
 
 
+def _plan(shapes, bits, gs, m=1):
+    import ctypes
+
+    from dequant_project_amd import _native
+    arr = (_native.DqGemvProblem * len(shapes))()
+    for i, (n, k) in enumerate(shapes):
+        arr[i].N, arr[i].K, arr[i].group_size = n, k, gs or k
+    wk, rows, kind = (ctypes.c_int * len(shapes))(), ctypes.c_int(), ctypes.c_int()
+    assert _native.capi().dq_gemv_plan(arr, len(shapes), m, bits, wk, ctypes.byref(rows), ctypes.byref(kind)) == 0
+    return list(wk), rows.value, kind.value
+
+
+@pytest.mark.parametrize("bits,gs,sym,layout,shapes,rows_per_tile", [
+    # INT4 g32 sym interleaved, 8-row tiles: ragged row counts (each problem's
+    # last block-tile has empty wave slots), K of 160 / 96 / 33 chunks (partial
+    # last batches), a one-row problem, and different x per problem
+    (4, 32, True, "interleaved", [(5003, 5120), (7001, 3072), (9999, 5120), (30005, 1056), (1, 5120),
+                                  (20000, 4096)], 8),
+    # INT4 g128 asym sequential, 4-row tiles (the decode gate | up launch)
+    (4, 128, False, "sequential", [(14336, 4096), (14336, 4096)], 4),
+    # INT8 per-channel sym interleaved, 4-row tiles, plus a five-row problem
+    (8, None, True, "interleaved", [(11008, 4096), (11008, 4096), (11008, 4096), (5, 4096)], 4),
+    # INT8 g64 asym sequential, 8-row tiles over K = 14336 (seven batches per tile)
+    (8, 64, False, "sequential", [(4100, 14336)] * 16, 8),
+])
+def test_pipelined_m1_kernel_walk(torch_gpu, bits, gs, sym, layout, shapes, rows_per_tile):
+    """gemv_m1_pipe_kernel (kind 4 of dq_gemv_plan): the walk that issues the
+    next batch's rows while the current batch is computed, crossing tiles and
+    problems, with the activations staged per block in pair order. Every
+    problem against the oracle on a sample of rows that includes its last 40,
+    and against its single call."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    wk, r, kind = _plan(shapes, bits, gs)
+    assert (wk, r, kind) == ([1] * len(shapes), rows_per_tile, 4)
+    gen = torch.Generator(device="cuda").manual_seed(bits * 7 + len(shapes))
+    cfg = QuantConfig(bits, gs, sym, layout)
+    pws, cases, xs, x16s = [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        pw = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02, cfg)
+        rng = np.random.Generator(np.random.PCG64(500 + i))
+        rows = np.unique(np.concatenate([rng.choice(n, min(n, 160), replace=False), np.arange(max(0, n - 40), n)]))
+        qw, sc = pw.qweight.cpu().numpy(), pw.scales.cpu().numpy()
+        ze = None if pw.zeros is None else pw.zeros.cpu().numpy()
+        cases.append(OracleCase(pw, qw, sc, ze, rows, deq_ref=False))
+        x16s.append(activations(1, k, seed=600 + i))
+        xs.append(to_gpu(torch, x16s[-1]))
+        pws.append(pw)
+    args = ([p.qweight for p in pws], [p.scales for p in pws], [p.zeros for p in pws], bits,
+            [p.config.effective_group_size(p.shape[1]) for p in pws], sym, layout == "interleaved")
+    ys = ext().gemv_batched(xs, *args)
+    again = ext().gemv_batched(xs, *args)
+    for i, (x, pw) in enumerate(zip(xs, pws)):
+        assert torch.equal(ys[i], again[i]), f"problem {i}: not deterministic"
+        cases[i].check(ys[i].cpu().numpy(), x16s[i], f"pipelined INT{bits} {shapes[i]} problem {i}")
+        single = ext().gemv(x, *ext_args(pw)).float()
+        diff = (ys[i].float() - single).norm() / single.norm().clamp_min(1e-30)
+        assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
+
+
 def test_int2_shared_and_mixed_activations_across_tiles(torch_gpu):
     """An INT2 launch of one-batch 8-row tiles over more than two rounds of
     the grid, the case where each wave runs a contiguous range of tiles and
@@ -734,3 +795,24 @@ def test_launch_event_hook_times_the_kernel(torch_gpu):
     ms = e0.elapsed_time(e1)
     assert 0.0 < ms < 50.0
     assert torch.equal(y, ext().gemv(x, *ext_args(pw)))  # the hook changes timing only
+
+
+def test_measurement_kernels(torch_gpu):
+    """dq_stream_read reads its buffer and leaves the sink alone for real
+    data; dq_empty_kernel launches; both validate their arguments."""
+    torch = torch_gpu
+    from dequant_project_amd import _native
+
+    lib = _native.capi()
+    stream = torch.cuda.current_stream().cuda_stream
+    buf = torch.randint(-2**31, 2**31 - 1, (1 << 24,), dtype=torch.int32, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    assert lib.dq_stream_read(buf.data_ptr(), buf.numel() * 4, sink.data_ptr(), stream) == 0
+    assert lib.dq_stream_read(buf.data_ptr(), 4096 + 16, sink.data_ptr(), stream) == 0  # a short tail
+    assert lib.dq_empty_kernel(stream) == 0
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
+    assert lib.dq_stream_read(buf.data_ptr(), 24, sink.data_ptr(), stream) == 1
+    assert b"multiple of 16" in lib.dq_last_error()
+    assert lib.dq_stream_read(buf.data_ptr() + 4, 32, sink.data_ptr(), stream) == 1
+    assert b"16-byte aligned" in lib.dq_last_error()
