@@ -11,10 +11,12 @@
 //               that do not need tensor metadata) and launch on `stream`.
 // Errors are reported as a status code plus a thread-local message.
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <sstream>
 #include <string>
+#include <vector>
 
 #include "dequant_hip.h"
 #include "dq_internal.h"
@@ -172,14 +174,55 @@ int check_extent(int64_t N, int64_t K) {
 }
 
 // The GEMV kernels address every operand with 32-bit buffer offsets and use
-// offsets at or above 2^31 as "out of range": each operand must stay below
-// 2 GiB (a Llama-3-70B down_proj is 0.45 GiB at INT8).
-int check_gemv_bytes(int64_t M, int64_t N, int64_t K, int64_t bits, int64_t group_size) {
-  constexpr int64_t kLimit = int64_t(1) << 31;
-  if (N * K / 8 * bits >= kLimit || N * (K / group_size) * 2 >= kLimit || M * K * 2 >= kLimit)
-    return fail(DQ_ERR_INVALID_ARGUMENT, cat("GEMV operands of shape [", N, ", ", K, "] (M=", M,
-                                             ") exceed the 2 GiB per-operand limit of the GEMV kernels"));
+// offsets at or above 2^31 as "out of range", so each operand of a launched
+// problem stays below 2 GiB. Weights past that (an INT8 lm_head of
+// 128256 x 16384 is 2.1 GB) are launched as row slices (slice_problems); the
+// activations, M x K fp16, must fit as they are.
+constexpr int64_t kOperandLimit = (int64_t(1) << 31) - 1;
+
+int check_gemv_bytes(int64_t M, int64_t K) {
+  if (M * K * 2 > kOperandLimit)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("x of shape [", M, ", ", K, "] exceeds the 2 GiB operand limit of ",
+                                             "the GEMV kernels"));
   return DQ_OK;
+}
+
+// Rows of one slice: every weight operand of the slice (qweight, scales,
+// zeros) below 2 GiB; a multiple of 64 rows when that leaves any.
+int64_t slice_rows(int64_t K, int64_t bits, int64_t group_size) {
+  const int64_t wrow = K * bits / 8, mrow = K / group_size * 2;
+  int64_t r = std::min(kOperandLimit / wrow, kOperandLimit / mrow);
+  if (r >= 64) r = r / 64 * 64;
+  return std::max<int64_t>(r, 1);
+}
+
+// `op` as row slices below the operand limit (one slice when it already is):
+// slice j holds rows [r0, r0 + n) of qweight, scales and zeros and writes
+// y[:, r0 : r0 + n], so its y row stride stays the whole problem's N.
+void append_slices(const dq::GemvOperand& op, int64_t bits, std::vector<dq::GemvOperand>& out) {
+  const int64_t rows = slice_rows(op.K, bits, op.group_size);
+  const int64_t words = op.K * bits / 32, groups = op.K / op.group_size;
+  for (int64_t r0 = 0; r0 < op.N; r0 += rows) {
+    dq::GemvOperand sl = op;
+    sl.N = std::min(rows, op.N - r0);
+    sl.qweight = op.qweight + r0 * words;
+    sl.scales = op.scales + r0 * groups;
+    sl.zeros = op.zeros ? op.zeros + r0 * groups : nullptr;
+    sl.y = op.y + r0;
+    sl.ldy = op.ldy ? op.ldy : op.N;
+    out.push_back(sl);
+  }
+}
+
+// Launches a list of problems (already sliced) in groups of at most
+// kMaxBatch; one launch unless slicing produced more problems than that.
+template <typename Launch>
+hipError_t launch_in_groups(const std::vector<dq::GemvOperand>& ops, Launch launch) {
+  for (size_t i = 0; i < ops.size(); i += dq::kMaxBatch) {
+    const hipError_t e = launch(ops.data() + i, static_cast<int>(std::min<size_t>(dq::kMaxBatch, ops.size() - i)));
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 // The scalar contract of one raw-pointer GEMV problem.
@@ -195,7 +238,7 @@ int check_gemv_problem(const uint16_t* x, const uint32_t* qweight, const uint16_
   if ((st = check_gemv_group(group_size, bits))) return st;
   if (!aligned16(qweight)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
   if ((st = check_extent(N, K))) return st;
-  return check_gemv_bytes(M, N, K, bits, group_size);
+  return check_gemv_bytes(M, K);
 }
 
 int launch_status(hipError_t e) {
@@ -251,7 +294,7 @@ int check_packed_product(const dq_tensor* x, const dq_tensor* qweight, const dq_
   // this implementation's own requirements
   if (!aligned16(qweight->data)) return fail(DQ_ERR_INVALID_ARGUMENT, "qweight must be 16-byte aligned");
   if ((st = check_extent(qweight->sizes[0], K))) return st;
-  return check_gemv_bytes(x->sizes[0], qweight->sizes[0], K, bits, group_size);
+  return check_gemv_bytes(x->sizes[0], K);
 }
 
 }  // namespace
@@ -300,9 +343,12 @@ int dq_gemv(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales, 
   if (st) return st;
   if ((st = check_gemv_problem(x, qweight, scales, zeros, y, M, N, K, bits, group_size, symmetric))) return st;
   if (N == 0) return DQ_OK;
-  const dq::GemvOperand op{x, qweight, scales, zeros, y, N, K, group_size};
-  return launch_status(dq::launch_gemv_batch(&op, 1, M, static_cast<int>(bits), symmetric != 0, interleaved != 0,
-                                             reinterpret_cast<hipStream_t>(stream)));
+  std::vector<dq::GemvOperand> ops;
+  append_slices(dq::GemvOperand{x, qweight, scales, zeros, y, N, K, group_size}, bits, ops);
+  return launch_status(launch_in_groups(ops, [&](const dq::GemvOperand* o, int n) {
+    return dq::launch_gemv_batch(o, n, M, static_cast<int>(bits), symmetric != 0, interleaved != 0,
+                                 reinterpret_cast<hipStream_t>(stream));
+  }));
 }
 
 int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
@@ -313,8 +359,7 @@ int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64
   if (!problems) return fail(DQ_ERR_INVALID_ARGUMENT, "problems must not be NULL");
   int st = check_m(M);
   if (st) return st;
-  dq::GemvOperand ops[DQ_MAX_BATCH];
-  int live = 0;
+  std::vector<dq::GemvOperand> ops;
   for (int i = 0; i < count; ++i) {
     const dq_gemv_problem& p = problems[i];
     if ((st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, M, p.N, p.K, bits, p.group_size,
@@ -322,11 +367,14 @@ int dq_gemv_batched(const dq_gemv_problem* problems, int count, int64_t M, int64
       g_error = cat("problem ", i, ": ", g_error);
       return st;
     }
-    if (p.N > 0) ops[live++] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
+    if (p.N > 0) append_slices(dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size},
+                               bits, ops);
   }
-  if (live == 0) return DQ_OK;
-  return launch_status(dq::launch_gemv_batch(ops, live, M, static_cast<int>(bits), symmetric != 0,
-                                             interleaved != 0, reinterpret_cast<hipStream_t>(stream)));
+  if (ops.empty()) return DQ_OK;
+  return launch_status(launch_in_groups(ops, [&](const dq::GemvOperand* o, int n) {
+    return dq::launch_gemv_batch(o, n, M, static_cast<int>(bits), symmetric != 0, interleaved != 0,
+                                 reinterpret_cast<hipStream_t>(stream));
+  }));
 }
 
 int dq_gemv_prologue_batched(const dq_gemv_problem* problems, const void* const* aux, int count, int64_t M,
@@ -341,8 +389,7 @@ int dq_gemv_prologue_batched(const dq_gemv_problem* problems, const void* const*
   if (prologue == DQ_PROLOGUE_RMSNORM && !(eps >= 0.0f && eps < 1e30f))
     return fail(DQ_ERR_INVALID_ARGUMENT, cat("eps must be finite and non-negative, got ", eps));
   if (M != 1) return fail(DQ_ERR_UNSUPPORTED, cat("fused prologues handle M = 1, got M=", M));
-  dq::GemvOperand ops[DQ_MAX_BATCH];
-  int live = 0;
+  std::vector<dq::GemvOperand> ops;
   for (int i = 0; i < count; ++i) {
     const dq_gemv_problem& p = problems[i];
     int st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, M, p.N, p.K, bits, p.group_size,
@@ -354,14 +401,16 @@ int dq_gemv_prologue_batched(const dq_gemv_problem* problems, const void* const*
       return st;
     }
     if (p.N > 0) {
-      ops[live] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
-      ops[live++].aux = static_cast<const uint16_t*>(aux[i]);
+      dq::GemvOperand op{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
+      op.aux = static_cast<const uint16_t*>(aux[i]);
+      append_slices(op, bits, ops);
     }
   }
-  if (live == 0) return DQ_OK;
-  return launch_status(dq::launch_gemv_prologue_batch(ops, live, M, static_cast<int>(bits), symmetric != 0,
-                                                      interleaved != 0, prologue, eps,
-                                                      reinterpret_cast<hipStream_t>(stream)));
+  if (ops.empty()) return DQ_OK;
+  return launch_status(launch_in_groups(ops, [&](const dq::GemvOperand* o, int n) {
+    return dq::launch_gemv_prologue_batch(o, n, M, static_cast<int>(bits), symmetric != 0, interleaved != 0,
+                                          prologue, eps, reinterpret_cast<hipStream_t>(stream));
+  }));
 }
 
 int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
@@ -372,8 +421,7 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
   if (!problems) return fail(DQ_ERR_INVALID_ARGUMENT, "problems must not be NULL");
   int st = check_gemm_m(M);
   if (st) return st;
-  dq::GemvOperand ops[DQ_MAX_BATCH];
-  int live = 0;
+  std::vector<dq::GemvOperand> ops;
   for (int i = 0; i < count; ++i) {
     const dq_gemv_problem& p = problems[i];
     if ((st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, M, p.N, p.K, bits, p.group_size,
@@ -381,11 +429,14 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
       g_error = cat("problem ", i, ": ", g_error);
       return st;
     }
-    if (p.N > 0) ops[live++] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
+    if (p.N > 0) append_slices(dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size},
+                               bits, ops);
   }
-  if (live == 0) return DQ_OK;
-  return launch_status(dq::launch_gemm_batch(ops, live, M, static_cast<int>(bits), symmetric != 0,
-                                             interleaved != 0, reinterpret_cast<hipStream_t>(stream)));
+  if (ops.empty()) return DQ_OK;
+  return launch_status(launch_in_groups(ops, [&](const dq::GemvOperand* o, int n) {
+    return dq::launch_gemm_batch(o, n, M, static_cast<int>(bits), symmetric != 0, interleaved != 0,
+                                 reinterpret_cast<hipStream_t>(stream));
+  }));
 }
 
 int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* waves_per_tile,

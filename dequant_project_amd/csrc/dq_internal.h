@@ -21,6 +21,7 @@ struct GemvOperand {
   uint16_t* y;              // fp16 [M, N]
   int64_t N, K, group_size;
   const uint16_t* aux = nullptr;  // prologue operand: RMSNorm gamma fp16 [K] or SwiGLU up fp16 [M, K]
+  int64_t ldy = 0;                // row stride of y in elements; 0 = N (a row slice of a larger problem sets it)
 };
 
 // Profiling hook: when both events are non-null, the next GEMV launch on this

@@ -251,6 +251,7 @@ struct KernelProblem {
   int lwk;               // log2 of the waves sharing one tile along K (wk = 1, 2 or 4)
   int per_wave;          // ceil(n_chunks / wk): chunks of one wave's share
   int tiles;             // ceil(N / R)
+  int ldy;               // row stride of y in elements (N unless the problem is a row slice of a larger one)
 };
 
 struct KernelBatch {
@@ -1433,7 +1434,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
       for (int v = 0; v < NV; ++v) {
         const int g = v / (MG * 4), m = 4 * ((v / 4) % MG) + (v % 4), n = t.row0 + 4 * g + q;
         if (blk == (v & 3) && t.active && m < b.M && n < d.N)
-          d.y[static_cast<int64_t>(m) * d.N + n] = f32_to_f16_rn(tot[v]);
+          d.y[static_cast<int64_t>(m) * d.ldy + n] = f32_to_f16_rn(tot[v]);
       }
     } else {
 #pragma unroll
@@ -1447,7 +1448,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
           if (blk == (v & 3) && m < b.M && n < d.N) {
             float s = 0.f;
             for (int j = 0; j < t.wk; ++j) s += part[phase][wave + j][v][q];
-            d.y[static_cast<int64_t>(m) * d.N + n] = f32_to_f16_rn(s);
+            d.y[static_cast<int64_t>(m) * d.ldy + n] = f32_to_f16_rn(s);
           }
         }
       }
@@ -1499,6 +1500,7 @@ struct GemmProblem {
   int lwk;        // log2 of the waves sharing one tile along K
   int per_wave;   // ceil(n_iters / wk)
   int tiles;      // ceil(N / 16)
+  int ldy;        // row stride of y in elements
 };
 
 struct GemmBatch {
@@ -1699,7 +1701,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_mfma_kernel(const GemmBatch b
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int m = 16 * mb + 4 * kb + i;
-          if (active && m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.N + ncol] = f32_to_f16_rn(acc[mb][i]);
+          if (active && m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.ldy + ncol] = f32_to_f16_rn(acc[mb][i]);
         }
     } else {
 #pragma unroll
@@ -1715,7 +1717,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_mfma_kernel(const GemmBatch b
             float v = 0.f;
             for (int j = 0; j < wk; ++j) v += part[phase][wave + j][4 * mb + i][lane];
             const int m = 16 * mb + 4 * kb + i;
-            if (m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.N + ncol] = f32_to_f16_rn(v);
+            if (m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.ldy + ncol] = f32_to_f16_rn(v);
           }
       }
       phase ^= 1;
@@ -1867,7 +1869,7 @@ __global__ void __launch_bounds__(256 * TPB) gemm_shared_x_kernel(const GemmBatc
           const float v = part[wave][4 * mb + i][lane] + part[wave + 1][4 * mb + i][lane] +
                           part[wave + 2][4 * mb + i][lane] + part[wave + 3][4 * mb + i][lane];
           const int m = 16 * mb + 4 * kb + i;
-          if (m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.N + ncol] = f32_to_f16_rn(v);
+          if (m < b.M && ncol < d.N) d.y[static_cast<int64_t>(m) * d.ldy + ncol] = f32_to_f16_rn(v);
         }
     }
     __syncthreads();  // the partials are read before the next tile writes them
@@ -2120,6 +2122,7 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
     k.lwk = log2_exact(wk);
     k.per_wave = ((k.n_chunks + wk - 1) / wk + step - 1) / step * step;
     k.tiles = static_cast<int>((o.N + R - 1) / R);
+    k.ldy = static_cast<int>(o.ldy ? o.ldy : o.N);
     const int tiles_per_bt = kWavesPerBlock / wk;
     kb.bt_start[i] = bts;
     bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;
@@ -2311,6 +2314,7 @@ hipError_t launch_gemm_mb(const GemvOperand* ops, int count, int64_t M, hipStrea
       k.lwk = log2_exact(wk);
       k.per_wave = (k.n_iters + wk - 1) / wk;
       k.tiles = static_cast<int>((o.N + 15) / 16);
+      k.ldy = static_cast<int>(o.ldy ? o.ldy : o.N);
       const int tiles_per_bt = waves_per_block / wk;
       gb.bt_start[i] = bts;
       bts += (k.tiles + tiles_per_bt - 1) / tiles_per_bt;

@@ -19,7 +19,11 @@ Numerics: RMSNorm is computed as (W (x * gamma)) / sqrt(mean(x^2) + eps) with
 fp32 sums and fp16 products x * gamma, where the unfused module rounds
 x / rms to fp16 and multiplies by gamma in fp16; SwiGLU rounds like the
 unfused fp16 ops (silu in fp32, rounded; times up, rounded). Both match the
-unfused composition to the fp16 rounding of the activations.
+unfused composition to the fp16 rounding of the activations. Valid input
+range of the RMSNorm prologue: every product x_i * gamma_i must be a finite
+fp16 value (|x_i * gamma_i| <= 65504), since it is formed before the
+division by rms(x); the unfused module divides first. Decoder residual
+streams (entries up to a few thousand, gamma of order one) are far inside it.
 """
 
 import torch
@@ -172,10 +176,16 @@ def _is_silu(act):
     return isinstance(act, nn.SiLU) or type(act).__name__ == "SiLUActivation"
 
 
+def _fmt(lin):
+    return lin.config.bits, lin.config.symmetric, lin.config.layout
+
+
 def _fusable_mlp(mlp):
+    """gate | up run as one grouped launch, so they must share bits, symmetry
+    and layout; down_proj is a launch of its own and may differ."""
     return (all(isinstance(getattr(mlp, n, None), QuantLinear) for n in ("gate_proj", "up_proj", "down_proj"))
             and _is_silu(getattr(mlp, "act_fn", None))
-            and len({getattr(mlp, n).config.bits for n in ("gate_proj", "up_proj", "down_proj")}) == 1)
+            and _fmt(mlp.gate_proj) == _fmt(mlp.up_proj))
 
 
 def fuse_llama(model):
@@ -190,8 +200,7 @@ def fuse_llama(model):
         if attn is None or not hasattr(layer, "input_layernorm"):
             continue
         qkv = [(r, getattr(attn, r, None)) for r in ("q_proj", "k_proj", "v_proj")]
-        if all(isinstance(lin, QuantLinear) for _, lin in qkv) and \
-                len({(lin.config.bits, lin.config.symmetric, lin.config.layout) for _, lin in qkv}) == 1:
+        if all(isinstance(lin, QuantLinear) for _, lin in qkv) and len({_fmt(lin) for _, lin in qkv}) == 1:
             pending = _Pending()
             layer.input_layernorm = _DeferredNorm(layer.input_layernorm, pending)
             group = list(qkv)

@@ -43,9 +43,22 @@ MAX_M_GEMM = 64
 GEMM_SMALL_MAX_CODES_ABOVE_32 = 1 << 25
 
 
-def uses_gemm_small(m, n, k):
-    """Whether QuantLinear runs the fused small GEMM for m rows of an [n, k] weight."""
-    return MAX_M < m <= MAX_M_GEMM and (m <= 32 or n * k <= GEMM_SMALL_MAX_CODES_ABOVE_32)
+def uses_gemm_small(m, n, k, cfg=None, x=None):
+    """Whether QuantLinear runs the fused small GEMM for m rows of an [n, k] weight.
+
+    Besides the measured size rule, the small GEMM takes the GEMV kernels'
+    operand rules: group_size a multiple of 128/bits codes (one 16-byte
+    chunk per group at least; INT2 g32 is excluded) and x 16-byte aligned.
+    Inputs outside them take the reference's dequantize + F.linear path,
+    which has neither restriction.
+    """
+    if not (MAX_M < m <= MAX_M_GEMM and (m <= 32 or n * k <= GEMM_SMALL_MAX_CODES_ABOVE_32)):
+        return False
+    if cfg is not None and cfg.effective_group_size(k) % (128 // cfg.bits) != 0:
+        return False
+    if x is not None and x.data_ptr() % 16 != 0:
+        return False
+    return True
 
 # The projections of a Llama-style decoder layer that quantize_model replaces.
 PROJ = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
@@ -144,7 +157,8 @@ class QuantLinear(nn.Module):
         m = x.numel() // self.in_features
         if m <= MAX_M:
             y = gemv(x, pw)
-        elif uses_gemm_small(m, self.out_features, self.in_features):
+        elif uses_gemm_small(m, self.out_features, self.in_features, self.config,
+                             x.reshape(-1, self.in_features).contiguous()):
             y = gemm_small(x, pw)
         else:
             y = F.linear(x, dequantize_cuda(pw))

@@ -131,7 +131,9 @@ int dq_check_unpack(const dq_tensor* qweight, int64_t bits, int64_t K);
  *   y        fp16 [M, N] output (written, never read)
  * group_size must divide K and be a multiple of 128/bits codes (one 16-byte
  * load), which excludes INT2 with group_size 32 (dequant_gemv.cu:357-361).
- * Each operand (qweight, scales/zeros, x) must be smaller than 2 GiB. */
+ * x must be smaller than 2 GiB. Weights of any size are taken: a weight whose
+ * qweight or scales reach 2 GiB (the kernels' 32-bit buffer offsets) is
+ * launched as row slices below that, writing disjoint columns of y. */
 int dq_gemv(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
             const uint16_t* zeros, uint16_t* y, int64_t M, int64_t N, int64_t K,
             int64_t bits, int64_t group_size, int symmetric, int interleaved,

@@ -53,3 +53,17 @@ def test_leaves_unfusable_layers_alone():
     mixed.model.layers[0].self_attn.k_proj = QuantLinear.from_linear(
         torch.nn.Linear(128, 64, bias=False).half(), QuantConfig(8, None, True))
     assert fuse_llama(mixed) == {"attention": 1, "mlp": 2}       # q|k|v must share one format
+
+
+def test_mlp_with_mixed_gate_up_formats_stays_unfused():
+    """gate | up go into one grouped launch, so they must share bits,
+    symmetry and layout; down_proj is a launch of its own and may differ."""
+    model = tiny(layers=2)
+    quantize_model(model, QuantConfig(4, 128, False))
+    mlp = model.model.layers[0].mlp
+    mlp.up_proj = QuantLinear.from_linear(torch.nn.Linear(128, 384, bias=False).half(), QuantConfig(4, 128, True))
+    model.model.layers[1].mlp.down_proj = QuantLinear.from_linear(
+        torch.nn.Linear(384, 128, bias=False).half(), QuantConfig(8, None, True))
+    assert fuse_llama(model) == {"attention": 2, "mlp": 1}
+    assert not isinstance(model.model.layers[0].mlp, _FusedMLP)
+    assert isinstance(model.model.layers[1].mlp, _FusedMLP)

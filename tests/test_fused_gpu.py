@@ -91,6 +91,35 @@ def test_gemv_swiglu_matches_oracle(torch_gpu, n, k, count):
             check(y.cpu().numpy(), [h64 @ w64.T, h16 @ w64.T], f"swiglu {fmt} [{n},{k}] problem {i}")
 
 
+@pytest.mark.parametrize("scale", ["residual", "tiny"])
+def test_gemv_rmsnorm_at_residual_stream_scales(torch_gpu, scale):
+    """RMSNorm prologue on inputs shaped like a decoder's residual stream: a
+    few outlier features in the thousands over N(0, 1) entries ("residual"),
+    and a row of magnitude ~1e-3 ("tiny"). The fused form rounds x * gamma to
+    fp16 before dividing by rms(x); both cases stay far inside fp16's range
+    (|x * gamma| <= 65504), so it must match the unfused module."""
+    torch = torch_gpu
+    from dequant_project_amd.fused import gemv_rmsnorm
+
+    n, k = 2048, 4096
+    g = rng(41 if scale == "residual" else 42)
+    x = g.standard_normal((1, k)).astype(np.float32)
+    if scale == "residual":
+        idx = g.choice(k, 8, replace=False)
+        x[0, idx] = np.sign(g.standard_normal(8)) * g.uniform(1000.0, 6000.0, 8)
+    else:
+        x *= 1e-3
+    x = x.astype(np.float16)
+    gamma = (1.0 + 0.2 * g.standard_normal(k)).astype(np.float16)
+    assert np.isfinite(x.astype(np.float32) * gamma.astype(np.float32)).all()
+    h64 = R.rmsnorm64(x, gamma, EPS)
+    h16 = R.rmsnorm_fp16(x, gamma, EPS).astype(np.float64)
+    for fmt in FORMATS:
+        (pw, w64), = packed_group(torch, n, k, 1, fmt, seed=43)
+        (y,) = gemv_rmsnorm(to_gpu(torch, x), to_gpu(torch, gamma), EPS, [pw])
+        check(y.cpu().numpy(), [h64 @ w64.T, h16 @ w64.T], f"rmsnorm {scale} {fmt}")
+
+
 def test_prologues_with_zero_points_beyond_fp16_exact_range(torch_gpu):
     """The kernels' separate path for zero points outside [-1024, 1024]
     re-reads the activations: it must apply the prologue too."""

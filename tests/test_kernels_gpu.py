@@ -816,3 +816,48 @@ def test_measurement_kernels(torch_gpu):
     assert b"multiple of 16" in lib.dq_last_error()
     assert lib.dq_stream_read(buf.data_ptr() + 4, 32, sink.data_ptr(), stream) == 1
     assert b"16-byte aligned" in lib.dq_last_error()
+
+
+@pytest.mark.parametrize("m", (1, 4, 16))
+def test_weights_past_two_gib_run_as_row_slices(torch_gpu, m):
+    """An INT8 per-channel weight of 140000 x 16384 (2.29 GB of qweight, past
+    the kernels' 32-bit buffer offsets; a 140k-token vocabulary's lm_head):
+    the C ABI launches it as two row slices (131008 rows, then the rest),
+    each writing its own columns of y with the whole y's row stride. Rows on both sides of the cut and the last
+    rows against the oracle, for the M = 1 kernel, the 2 <= M <= 8 kernel and
+    the small GEMM."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    n, k = 140000, 16384
+    gen = torch.Generator(device="cuda").manual_seed(77)
+    w = torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02
+    pw = quantize_tensor(w, QuantConfig(8, None, True))
+    del w
+    assert pw.qweight.numel() * 4 >= 2 ** 31
+    rows = np.unique(np.concatenate([np.arange(0, 24), np.arange(131000, 131016), np.arange(n - 40, n),
+                                     np.random.Generator(np.random.PCG64(78)).choice(n, 64, replace=False)]))
+    ridx = torch.from_numpy(rows).cuda()
+    qw = pw.qweight[ridx].cpu().numpy()
+    sc = pw.scales[ridx].cpu().numpy()
+    cfg = P.Config(8, None, True, "sequential")
+    # the GEMV multiplies by exact (q - z) * s; the small GEMM, like the
+    # reference's M > 8 path, by packer.dequantize's fp16 weight
+    if m <= 8:
+        w64 = P.exact_weight(qw, sc, None, cfg, (len(rows), k)).astype(np.float64)
+    else:
+        w64 = P.dequantize(qw, sc, None, cfg, (len(rows), k)).astype(np.float64)
+    x16 = activations(m, k, seed=79)
+    x = to_gpu(torch, x16)
+    if m <= 8:
+        y = ext().gemv(x, *ext_args(pw))
+    else:
+        y = ext().gemm_small(x, *ext_args(pw))
+    assert tuple(y.shape) == (m, n)
+    y = y[:, ridx].cpu().numpy()
+    x64 = x16.astype(np.float64)
+    ref, absref = x64 @ w64.T, np.abs(x64) @ np.abs(w64).T
+    ok, worst = P.gemv_criterion(y, ref, absref)
+    print(f"2.29 GB INT8 weight M={m}: worst={worst:.3f}x tol rel_l2={P.rel_l2(y, ref):.2e}", flush=True)
+    assert ok, f"elementwise criterion violated, worst {worst:.3f}x"
+    assert P.rel_l2(y, ref) <= REL_L2_TOL

@@ -177,8 +177,47 @@ def test_quant_linear_against_f_linear(torch_gpu, shape):
     xf = x.float().reshape(m, k)
     ref = xf @ w_ref.T + ql.bias.float()
     absref = xf.abs() @ w_ref.abs().T
-    path = "gemv" if m <= MAX_M else ("gemm_small" if uses_gemm_small(m, n, k) else "fallback")
+    path = "gemv" if m <= MAX_M else ("gemm_small" if uses_gemm_small(m, n, k, ql.config) else "fallback")
     _check(y.reshape(m, n), ref, absref, 2, f"QuantLinear {shape} M={m} via {path}")
+
+
+def test_gemm_small_routing_respects_operand_rules():
+    """uses_gemm_small (host logic): 9..64-row inputs go to the fused small
+    GEMM only when its operand rules hold; INT2 with group 32 (a 16-byte
+    chunk is 64 INT2 codes) and misaligned x take dequantize + F.linear."""
+    from dequant_project_amd.quant_linear import uses_gemm_small
+
+    assert uses_gemm_small(16, 1024, 3072, QuantConfig(4, 128, False))
+    assert not uses_gemm_small(16, 1024, 3072, QuantConfig(2, 32, False))
+    assert not uses_gemm_small(48, 1024, 3072, QuantConfig(2, 32, True))
+    assert uses_gemm_small(48, 1024, 3072, QuantConfig(2, 64, True))
+    assert not uses_gemm_small(8, 1024, 3072, QuantConfig(4, 128, False))      # the GEMV's range
+    assert not uses_gemm_small(65, 1024, 3072, QuantConfig(4, 128, False))
+    x = torch.zeros(16 * 3072 + 1, dtype=torch.float16)[1:].view(16, 3072)     # 2-byte offset
+    assert not uses_gemm_small(16, 1024, 3072, QuantConfig(4, 128, False), x)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [16, 48])
+def test_quant_linear_int2_group32_batches_take_the_fallback(torch_gpu, m):
+    """INT2 g32 at 9..64 rows: the reference's dequantize + F.linear path
+    (the fused small GEMM cannot take this format); same product as the
+    reference's M > 8 branch, elementwise criterion against fp64."""
+    from dequant_project_amd.quant_linear import uses_gemm_small
+
+    torch.manual_seed(0)
+    k, n = 3072, 1024
+    lin = nn.Linear(k, n, bias=False).to("cuda", torch.float16)
+    cfg = QuantConfig(2, 32, False)
+    ql = QuantLinear.from_linear(lin, cfg)
+    assert not uses_gemm_small(m, n, k, cfg)
+    pw = ql._packed()
+    x = torch.randn(m, k, dtype=torch.float16, device="cuda")
+    with torch.no_grad():
+        y = ql(x)
+    w_ref = packer.dequantize(pw).float()
+    xf = x.float()
+    _check(y, xf @ w_ref.T, xf.abs() @ w_ref.abs().T, 1, f"QuantLinear INT2 g32 M={m} via fallback")
 
 
 @pytest.mark.gpu
