@@ -1959,29 +1959,31 @@ add_one_kernel(const float* __restrict__ in, float* __restrict__ out, int64_t n)
 // The benchmark's denominators (no reference counterpart in the kernels; the
 // reference measures its read ceiling with torch ops,
 // scripts/bandwidth_by_dtype.py:85-106):
-//   stream_read_kernel  reads `n16` 16-byte elements once, 1 KiB per wave and
-//                       load, eight loads in flight per lane, non-temporal
-//                       (the GEMV weights' policy): the practical HBM read
-//                       ceiling of a plain streaming read;
+//   stream_read_kernel  reads `bytes` once: wave w reads 1 KiB segments w,
+//                       w + W, w + 2W, ... (W waves in the grid) with one
+//                       non-temporal 16-byte load per lane, so the whole chip
+//                       sweeps the buffer in address order. Of the layouts
+//                       measured on the part (1-8 KiB per wave and load set,
+//                       2-8 waves per SIMD, strided or contiguous), this one
+//                       read fastest (~90% of the 8 TB/s peak over 4 GiB);
 //   empty_kernel        does nothing: the per-launch gap of back-to-back
 //                       launches in a HIP graph.
 // The xor of everything read decides one store that a real buffer never
 // triggers, so the loads cannot be dropped.
 constexpr uint32_t kReadMagic = 0x9e3779b9u;
 
-__global__ void __launch_bounds__(256) stream_read_kernel(const u32x4* __restrict__ src, int64_t n16,
+__global__ void __launch_bounds__(256) stream_read_kernel(const unsigned char* __restrict__ src, int64_t bytes,
                                                           uint32_t* __restrict__ sink) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * 4 + (threadIdx.x >> 6)));
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * 4;
+  const int64_t segments = (bytes + 1023) / 1024;
   u32x4 acc = {0u, 0u, 0u, 0u};
-  for (; i + 7 * stride < n16; i += 8 * stride) {
-    u32x4 v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) acc ^= v[u];
+  for (int64_t sg = wave; sg < segments; sg += waves) {
+    const int64_t left = bytes - sg * 1024;  // the last segment may be partial: loads past it return zeros
+    const __amdgpu_buffer_rsrc_t r = buffer_of(src + sg * 1024, static_cast<uint32_t>(left < 1024 ? left : 1024));
+    acc ^= __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<uint32_t>(lane) * 16u, 0, 2);
   }
-  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == kReadMagic && acc.x == kReadMagic) sink[0] = acc.y;
 }
 
@@ -2163,14 +2165,39 @@ constexpr bool m1_keeps_x(int bits) { return bits == 2; }
 constexpr int kKeepRun = 3;
 constexpr int kKeepRounds = 2;
 
-// The software-pipelined M = 1 kernel (gemv_m1_pipe_kernel) for launches of
-// one-wave tiles (wk = 1 for every problem: no barrier in its walk), INT4 and
-// INT8; INT2 launches keep their activation staging / keeping variants.
-bool m1_pipelined(int bits, const int* wks, int count) {
-  if (bits == 2) return false;
-  for (int i = 0; i < count; ++i)
-    if (wks[i] != 1) return false;
-  return true;
+// Which M = 1 kernel variant a launch runs (PRO = none; prologue launches
+// always take gemv_m1_kernel's load variant):
+//   kM1Stage  INT2, activations staged per block (conditions above), needs
+//             at least xl_rounds(R) rounds of its grid;
+//   kM1Keep   INT2, 8-row one-batch tiles, activations kept across tiles,
+//             needs kKeepRounds rounds of its grid;
+//   kM1Pipe   gemv_m1_pipe_kernel: every other launch of one-wave tiles
+//             (wk = 1 for every problem, so its walk has no barrier). On the
+//             INT2 launches outside the two variants above (the C4 decode
+//             gate | up launch: 4-row tiles) it measured 13% faster than the
+//             load variant (C4 INT2 decode 1.04 -> 0.905 ms/step); on the
+//             INT2 stack it ties the staged/kept variants, which keep those
+//             launches;
+//   kM1Load   gemv_m1_kernel, activations loaded per wave (split-K launches).
+// grid_stage / grid_keep: the co-resident blocks of the staged / kept kernels.
+enum M1Variant : int { kM1Load = 2, kM1Pipe = 4, kM1Stage = 5, kM1Keep = 6 };
+
+M1Variant m1_variant(const KernelBatch& kb, int count, int bits, int R, const int* wks, int bts, int grid_stage,
+                     int grid_keep) {
+  bool one_wave = true;
+  for (int i = 0; i < count; ++i) one_wave = one_wave && wks[i] == 1;
+  if (!one_wave) return kM1Load;
+  if (m1_stages_x(bits)) {
+    bool stage = true;
+    for (int i = 0; i < count; ++i) stage = stage && kb.p[i].n_chunks >= 2 * 64;
+    if (stage && bts >= xl_rounds(R) * grid_stage) return kM1Stage;
+  }
+  if (m1_keeps_x(bits) && R == 8) {
+    bool keep = true;
+    for (int i = 0; i < count; ++i) keep = keep && kb.p[i].n_chunks <= 64;
+    if (keep && bts >= kKeepRounds * grid_keep) return kM1Keep;
+  }
+  return kM1Pipe;
 }
 
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
@@ -2181,25 +2208,27 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
   const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
   kb.eps = eps;
   if (bts == 0) return hipSuccess;
-  if constexpr (m1_stages_x(BITS) && PRO == kProNone) {
-    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, kXmStage>;
-    bool stage = true;
-    for (int i = 0; i < count; ++i) stage = stage && wks[i] == 1 && kb.p[i].n_chunks >= 2 * 64;
-    const int grid = resident_blocks<kernel>();
-    if (stage && bts >= xl_rounds(R) * grid) return launch_kernel(kernel, grid, kb, stream);
-  }
-  if constexpr (m1_keeps_x(BITS) && PRO == kProNone && !m1_uses_mfma(BITS) && R == 8) {
-    constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, false, PRO, kXmKeep>;
-    bool keep = true;
-    for (int i = 0; i < count; ++i) keep = keep && wks[i] == 1 && kb.p[i].n_chunks <= 64;
-    const int grid = resident_blocks<kernel>();
-    kb.run = kKeepRun;
-    if (keep && bts >= kKeepRounds * grid) return launch_kernel(kernel, grid, kb, stream);
-  }
-  if constexpr (PRO == kProNone) {
-    if (m1_pipelined(BITS, wks, count)) {
-      constexpr auto kernel = gemv_m1_pipe_kernel<BITS, SYM, INTER, R>;
-      return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+  if constexpr (PRO == kProNone && !m1_uses_mfma(BITS)) {
+    constexpr auto stage_kernel = gemv_m1_kernel<BITS, SYM, INTER, R, false, PRO, kXmStage>;
+    constexpr auto keep_kernel = gemv_m1_kernel<BITS, SYM, INTER, R, false, PRO, kXmKeep>;
+    const int grid_stage = m1_stages_x(BITS) ? resident_blocks<stage_kernel>() : 0;
+    const int grid_keep = m1_keeps_x(BITS) && R == 8 ? resident_blocks<keep_kernel>() : 0;
+    switch (m1_variant(kb, count, BITS, R, wks, bts, grid_stage, grid_keep)) {
+      case kM1Stage:
+        if constexpr (m1_stages_x(BITS)) return launch_kernel(stage_kernel, grid_stage, kb, stream);
+        break;
+      case kM1Keep:
+        if constexpr (m1_keeps_x(BITS) && R == 8) {
+          kb.run = kKeepRun;
+          return launch_kernel(keep_kernel, grid_keep, kb, stream);
+        }
+        break;
+      case kM1Pipe: {
+        constexpr auto kernel = gemv_m1_pipe_kernel<BITS, SYM, INTER, R>;
+        return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+      }
+      default:
+        break;
     }
   }
   constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, kXmLoad>;
@@ -2453,7 +2482,19 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
   *mfma = M == 1 ? (m1_uses_mfma(bits) ? 3 : 2) : 0;
   *rows = rows_per_tile(ops, count);
   waves_per_tile(ops, count, bits, *rows, wk);
-  if (M == 1 && m1_pipelined(bits, wk, count)) *mfma = 4;
+  if (M == 1 && !m1_uses_mfma(bits)) {
+    // the INT2 staged / kept variants hold four blocks per CU; the launch
+    // itself asks the device for its kernel's co-resident blocks
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+      (void)hipGetLastError();
+      cus = 256;
+    }
+    KernelBatch kb;
+    const int bts = fill_kernel_batch(ops, count, M, bits, *rows, 1, wk, kb);
+    *mfma = m1_variant(kb, count, bits, *rows, wk, bts, 4 * cus, 4 * cus);
+  }
 }
 
 void set_launch_events(hipEvent_t start, hipEvent_t stop) {
@@ -2507,8 +2548,8 @@ hipError_t launch_unpack(const uint32_t* qweight, int32_t* out, int64_t N, int64
 
 hipError_t launch_stream_read(const void* data, int64_t bytes, uint32_t* sink, hipStream_t stream) {
   const int grid = resident_blocks<stream_read_kernel>();
-  hipLaunchKernelGGL(stream_read_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const u32x4*>(data), bytes / 16,
-                     sink);
+  hipLaunchKernelGGL(stream_read_kernel, dim3(grid), dim3(256), 0, stream, static_cast<const unsigned char*>(data),
+                     bytes, sink);
   return hipGetLastError();
 }
 

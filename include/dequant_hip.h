@@ -215,13 +215,17 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
  *                      rows_per_tile, true> (M = 1; dot products on the
  *                      matrix cores; not chosen by the current geometry),
  *   *kernel_kind == 4: gemv_m1_pipe_kernel<bits, symmetric, interleaved,
- *                      rows_per_tile> (M = 1, INT4 and INT8 launches whose
- *                      tiles are all one wave wide: the next batch's loads
- *                      are issued while the current batch is computed).
- * Large INT2 launches of one-wave tiles with K >= 8192 take the M = 1
- * kernel's variant that stages the activations per block in LDS, those of
- * 8-row one-batch tiles (K <= 4096) the variant that keeps each wave's
- * activations across consecutive tiles (both still kind 2).
+ *                      rows_per_tile> (M = 1, launches whose tiles are all
+ *                      one wave wide: the next batch's loads are issued while
+ *                      the current batch is computed),
+ *   *kernel_kind == 5: gemv_m1_kernel's INT2 variant that stages each batch's
+ *                      activations per block in LDS (one-wave tiles, K >= 8192,
+ *                      enough rounds of its persistent grid),
+ *   *kernel_kind == 6: gemv_m1_kernel's INT2 variant that keeps a wave's
+ *                      activations across consecutive 8-row one-batch tiles
+ *                      (K <= 4096, at least two rounds of its grid).
+ * Kinds 5 and 6 depend on the device's co-resident blocks; without a device
+ * the plan assumes 256 CUs.
  * The geometry is chosen per launch, so a problem's result is deterministic
  * for a given launch but may differ in the last bits between a grouped launch
  * and a single one. waves_per_tile must hold `count` ints. */
@@ -262,8 +266,9 @@ int dq_add_one(const float* in, float* out, int64_t n, dq_stream_t stream);
  * torch ops, scripts/bandwidth_by_dtype.py:85-106, and quotes it in
  * hardware.md:71-100):
  *   dq_stream_read   reads `bytes` (a multiple of 16; data 16-byte aligned)
- *                    once, non-temporal, 1 KiB per wave and load: the
- *                    practical HBM read ceiling. sink (>= 4 bytes of device
+ *                    once, non-temporal, the chip sweeping the buffer in
+ *                    address order in 1 KiB wave loads: the practical HBM
+ *                    read ceiling. sink (>= 4 bytes of device
  *                    memory) is written only for a data pattern that real
  *                    buffers do not produce; it exists so the loads cannot
  *                    be dropped;

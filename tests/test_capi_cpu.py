@@ -222,7 +222,9 @@ def test_gemv_plan_geometry():
     assert plan([(14336, 4096)] * 16) == ([1] * 16, 8, 4)       # a stack of projections: 8-row tiles
     assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 4)
     assert plan([(4096, 14336)] * 16, bits=8, gs=None) == ([1] * 16, 8, 4)
-    assert plan([(14336, 4096)] * 16, bits=2, gs=64) == ([1] * 16, 8, 2)  # INT2: its own activation variants
+    assert plan([(14336, 4096)] * 16, bits=2, gs=64) == ([1] * 16, 8, 6)  # INT2: activations kept across tiles
+    assert plan([(14336, 8192)] * 16, bits=2, gs=64) == ([1] * 16, 8, 5)  # INT2: activations staged per block
+    assert plan([(14336, 4096)] * 2, bits=2, gs=64) == ([1, 1], 4, 4)     # INT2 decode gate | up: pipelined
     assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 2)  # 172 columns of 64 codes, 43 per wave
     assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 2)  # INT8 wants 8192 waves
     # 2 <= M <= 8: gemv_quad_kernel (kind 1) for every format and group size;

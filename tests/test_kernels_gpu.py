@@ -688,6 +688,10 @@ def _plan(shapes, bits, gs, m=1):
     (8, None, True, "interleaved", [(11008, 4096), (11008, 4096), (11008, 4096), (5, 4096)], 4),
     # INT8 g64 asym sequential, 8-row tiles over K = 14336 (seven batches per tile)
     (8, 64, False, "sequential", [(4100, 14336)] * 16, 8),
+    # INT2 g64 asym, 4-row tiles: the C4 decode gate | up launch
+    (2, 64, False, "sequential", [(14336, 4096), (14336, 4096)], 4),
+    # INT2 g128 sym interleaved, 4-row tiles, K of 120 / 64 / 2 chunks, ragged rows
+    (2, 128, True, "interleaved", [(9001, 7680), (5003, 4096), (777, 128), (2, 7680), (3000, 4096)], 4),
 ])
 def test_pipelined_m1_kernel_walk(torch_gpu, bits, gs, sym, layout, shapes, rows_per_tile):
     """gemv_m1_pipe_kernel (kind 4 of dq_gemv_plan): the walk that issues the
@@ -768,7 +772,7 @@ def test_int2_shared_and_mixed_activations_across_tiles(torch_gpu):
         arr[i].N, arr[i].K, arr[i].group_size = n, k, 64
     wk, rows_per_tile, kind = (ctypes.c_int * len(plan))(), ctypes.c_int(), ctypes.c_int()
     assert _native.capi().dq_gemv_plan(arr, len(plan), 1, 2, wk, ctypes.byref(rows_per_tile), ctypes.byref(kind)) == 0
-    assert (list(wk), rows_per_tile.value, kind.value) == ([1] * len(plan), 8, 2)
+    assert (list(wk), rows_per_tile.value, kind.value) == ([1] * len(plan), 8, 6)
     assert sum((n + 7) // 8 for n, _, _ in plan) // 4 >= 2 * 4 * 256
     ys = ext().gemv_batched(xs, [p.qweight for p in pws], [p.scales for p in pws], [p.zeros for p in pws], 2,
                             [p.config.effective_group_size(p.shape[1]) for p in pws], False, False)
