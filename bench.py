@@ -37,18 +37,22 @@ Measurement protocol (why the timed replays see the steady state):
     ceiling (a measurement of its own, reported below, long enough to cover
     that ramp); the headline stack follows immediately with its W warm-up
     and K timed replays.
-  * roofline.achieved is the dominant kernel's own duration: after the timed
-    legs, the headline's launches run eagerly STEPS times with the engine's
-    launch-event hook (hipExtLaunchKernelGGL start/stop events on the launch
-    stream), i.e. the figure rocprofv3's kernel trace reports.
+  * roofline.achieved is the dominant kernel's own duration: a leg replays
+    the stack step five times per graph (70 launches back to back, so the
+    per-replay launch overhead is spread thin), and replay time / launches is
+    the mean launch duration, the figure rocprofv3's kernel trace reports
+    for graph-replayed kernels (dequant_project_amd/traces.py summarizes that
+    trace per leg). The launch-event hook (hipExtLaunchKernelGGL start/stop
+    events around each eager launch) is reported beside it.
 
 Printed: ONE JSON line on stdout (progress goes to stderr).
   value            stack-mode algorithmic bytes per step / step time, GB/s
                    (the byte_model accounting: packed weights + scales +
                    zeros + x + y)
   roofline         the headline's kernel: algorithmic bytes per launch / its
-                   mean kernel duration; traffic from the committed rocprofv3
-                   FETCH_SIZE + WRITE_SIZE summary of that kernel (static)
+                   mean kernel duration; traffic: HBM bytes per launch from the
+                   committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the
+                   counter pass (a static figure, not measured in this run)
   ceilings         measured streaming-read ceiling and empty-kernel gap
   cpu_baseline     the reference's CPU torch path (oracle/cpu_path.py) on the
                    host cores: C4 one layer (value), rows for C1-C5, 1 thread
@@ -66,6 +70,10 @@ Printed: ONE JSON line on stdout (progress goes to stderr).
                    (scripts/bench_dequant_kernel.py:61-78, 119-168)
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+  python bench.py --counters --calibrate-copy --no-cpu-baseline --steps 2
+      the counter pass for rocprofv3 --pmc runs (no graphs, no timing;
+      dequant_project_amd/counters.py turns two such runs into the traffic
+      summary)
 """
 
 import argparse
@@ -95,7 +103,7 @@ CEILING_BYTES = 4 * 2 ** 30      # streaming-read ceiling buffer
 CEILING_WARM, CEILING_REPS = 20, 40
 EMPTY_LAUNCHES = 1000
 LAUNCH_LEG_STEPS = 5             # stack steps per replay of the launch-duration leg
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_m1_pipe_kernel_int4_c4_stack_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "dq_kernels_bench_legs_traffic.md")
 
 # a Llama-3-70B-shape stack in mixed precision
 C5_LAYERS = 80
@@ -125,7 +133,12 @@ def parse_args():
     ap.add_argument("--modes", default="stack,decode,per_linear",
                     help="comma-separated step structures to time (stack is the headline)")
     ap.add_argument("--calibrate-copy", action="store_true",
-                    help="also run a 1 GiB device copy (rocprof FETCH_SIZE/WRITE_SIZE calibration)")
+                    help="also run a 1 GiB device copy, the engine's add_one kernel (rocprof FETCH_SIZE / "
+                         "WRITE_SIZE calibration)")
+    ap.add_argument("--counters", action="store_true",
+                    help="counter pass for rocprofv3 --pmc runs: every leg's step run eagerly STEPS times (no "
+                         "graphs, no timing), an empty kernel before each leg as a delimiter; prints the "
+                         "algorithmic bytes of every launch in order")
     return ap.parse_args()
 
 
@@ -185,6 +198,9 @@ class Engine:
 
     def empty_kernel(self):
         self.native.check(self.capi.dq_empty_kernel(self.stream()))
+
+    def add_one(self, src, dst):
+        self.native.check(self.capi.dq_add_one(src.data_ptr(), dst.data_ptr(), src.numel(), self.stream()))
 
 
 # ----------------------------------------------------------------- building
@@ -273,14 +289,22 @@ def capture(torch, fn):
 
 # ------------------------------------------------------------------ timing
 class Leg:
-    """One timed leg: a captured graph replayed `warmup` times, then `steps`
-    times between events. Replays are only enqueued here; `result` reads the
-    events after the single synchronization that ends the timed phase."""
+    """One timed leg: the step function `fn` captured in a graph, replayed
+    `warmup` times, then `steps` times between events. Replays are only
+    enqueued here; `result` reads the events after the single synchronization
+    that ends the timed phase. `launch_bytes`: the algorithmic bytes of each
+    kernel launch of one step, in launch order (the counter pass maps them to
+    the profiler's dispatches). With Leg.eager set (the counter pass) nothing
+    is captured: the pass calls `fn` directly."""
 
-    def __init__(self, torch, name, graph, steps, warmup, step_bytes=None, meta=None, layers=None):
-        self.torch, self.name, self.graph = torch, name, graph
+    eager = False
+
+    def __init__(self, torch, name, fn, steps, warmup, step_bytes=None, meta=None, layers=None, launch_bytes=None):
+        self.torch, self.name, self.fn = torch, name, fn
+        self.graph = None if Leg.eager else capture(torch, fn)
         self.steps, self.warmup = steps, warmup
         self.step_bytes, self.meta, self.layers = step_bytes, meta or {}, layers
+        self.launch_bytes = launch_bytes
         self.evs = None
 
     def enqueue(self):
@@ -314,7 +338,7 @@ def gemv_leg(torch, eng, name, launches, steps, warmup, layers):
 
     meta = {"launches_per_step": len(launches),
             "kernel_instances": {k: len(v) for k, v in kernel_instances(eng, launches).items()}}
-    return Leg(torch, name, capture(torch, fn), steps, warmup, step_bytes, meta, layers)
+    return Leg(torch, name, fn, steps, warmup, step_bytes, meta, layers, [launch_bytes(x, p) for _, x, p in launches])
 
 
 def kernel_durations(torch, eng, launches, reps):
@@ -356,18 +380,19 @@ def kernel_durations(torch, eng, launches, reps):
     return out[1:]
 
 
-def profiled_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (copy-calibrated), or None if that summary is of
-    another kernel."""
+def profiled_traffic(kernel, leg="C4 stack"):
+    """HBM bytes per launch of `kernel` in `leg` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of the counter pass (copy-calibrated,
+    dequant_project_amd/counters.py), or None if it holds no such record."""
     try:
         text = open(TRAFFIC_PROFILE).read()
-        rec = json.loads(text.split("```json", 1)[1].split("```", 1)[0])
-    except (OSError, IndexError, ValueError):
+        recs = json.loads(text.split("```json", 1)[1].split("```", 1)[0])["records"]
+    except (OSError, IndexError, ValueError, KeyError):
         return None, None
-    if rec.get("kernel") != kernel:
-        return None, None
-    return rec["traffic_bytes_per_launch"], rec
+    for rec in recs:  # the engine names instances without the trailing default template arguments
+        if rec["leg"] == leg and (rec["kernel"] == kernel or rec["kernel"].startswith(kernel[:-1] + ",")):
+            return rec["traffic_bytes_per_launch"], rec
+    return None, None
 
 
 # ------------------------------------------------------------ extra legs
@@ -441,25 +466,34 @@ def single_copies(torch, n, k, cfg, seed, outliers=False):
                       for _ in range(copies - 1)]
 
 
-def gemm_stack(torch, stack, m, steps, warmup):
+def gemm_stack_leg(torch, stack, m, steps, warmup):
     """The fused small GEMM (quant_linear.gemm_small) over every projection of
-    the stack at m rows (a prefill chunk through all layers), in one graph,
-    against the reference's M > 8 path (dequantize + F.linear) timed eagerly
-    with HIP events (each of its GEMMs is tens of microseconds)."""
-    import torch.nn.functional as F
-
-    from dequant_project_amd.quant_linear import dequantize_cuda, gemm_small
+    the stack at m rows (a prefill chunk through all layers) as one leg, and
+    its items (x, weight)."""
+    from dequant_project_amd.quant_linear import gemm_small
 
     gen = torch.Generator(device="cuda").manual_seed(20251204 + m)
     xs = {k: torch.randn(m, k, generator=gen, device="cuda", dtype=torch.float16) for k in (HIDDEN, INTER)}
     items = [(xs[p.shape[1]], p) for layer in stack for _, p in sorted(layer.items())]
-    step_bytes = sum(launch_bytes([x], [p]) for x, p in items)
+    per_launch = [launch_bytes([x], [p]) for x, p in items]
 
     def fused():
         for x, p in items:
             gemm_small(x, p)
 
-    leg = Leg(torch, f"gemm M={m}", capture(torch, fused), steps, warmup, step_bytes, layers=len(stack))
+    return Leg(torch, f"gemm M={m}", fused, steps, warmup, sum(per_launch), layers=len(stack),
+               launch_bytes=per_launch), items
+
+
+def gemm_stack(torch, stack, m, steps, warmup):
+    """gemm_stack_leg timed in one graph, against the reference's M > 8 path
+    (dequantize + F.linear) timed eagerly with HIP events (each of its GEMMs
+    is tens of microseconds)."""
+    import torch.nn.functional as F
+
+    from dequant_project_amd.quant_linear import dequantize_cuda
+
+    leg, items = gemm_stack_leg(torch, stack, m, steps, warmup)
     leg.enqueue()
 
     def reference():
@@ -490,14 +524,8 @@ FORMAT_SHAPES = [("q/o_proj", HIDDEN, HIDDEN), ("k/v_proj", KV, HIDDEN), ("gate/
                  ("down_proj", HIDDEN, INTER)]
 
 
-def format_axis(torch, eng, steps, warmup):
-    """The reference's microbenchmark (scripts/bench_dequant_kernel.py:61-78,
-    119-168) on the Llama-3-8B projection shapes: per (shape, format) a graph
-    of n_copies = max(32, ceil(8 x 256 MB / bytes)) back-to-back calls over
-    distinct copies, M = 1; per-call time = replay time / n_copies (median,
-    p25, p75 over the timed replays); fp16 F.linear over the fp16 weight is
-    the row every speed-up is measured against. Every pair is built and
-    captured first, then all are timed back to back."""
+def format_axis_legs(torch, eng, steps, warmup):
+    """The legs of format_axis: one per (shape, format)."""
     import torch.nn.functional as F
 
     from dequant_project_amd import byte_model as bm
@@ -531,8 +559,21 @@ def format_axis(torch, eng, steps, warmup):
                         eng.gemv_group([x], [p])
                 call_bytes = bm.gemv_call_bytes(n, k, cfg.bits, cfg.group_size, cfg.symmetric, 1)
                 kernel = eng.kernel_name([x], [first])[0]
-            leg = Leg(torch, f"{label} {fmt}", capture(torch, fn), steps, warmup)
+            leg = Leg(torch, f"{label} {fmt}", fn, steps, warmup, launch_bytes=None if spec is None else
+                      [call_bytes] * copies)
             pairs.append((label, n, k, fmt, copies, call_bytes, kernel, leg, ws))
+    return pairs
+
+
+def format_axis(torch, eng, steps, warmup):
+    """The reference's microbenchmark (scripts/bench_dequant_kernel.py:61-78,
+    119-168) on the Llama-3-8B projection shapes: per (shape, format) a graph
+    of n_copies = max(32, ceil(8 x 256 MB / bytes)) back-to-back calls over
+    distinct copies, M = 1; per-call time = replay time / n_copies (median,
+    p25, p75 over the timed replays); fp16 F.linear over the fp16 weight is
+    the row every speed-up is measured against. Every pair is built and
+    captured first, then all are timed back to back."""
+    pairs = format_axis_legs(torch, eng, steps, warmup)
     torch.cuda.synchronize()
     for p in pairs:
         p[7].enqueue()
@@ -549,6 +590,41 @@ def format_axis(torch, eng, steps, warmup):
                      "floor_us": call_bytes / (PEAK_GBS * 1e9) * 1e6, "speedup_vs_fp16": base[label] / us,
                      "kernel": kernel})
     return rows
+
+
+# ------------------------------------------------------------ counter pass
+def counter_pass(torch, args, eng, stack, ceiling, legs):
+    """The kernels of every leg, run eagerly for rocprofv3 counter collection
+    (--pmc FETCH_SIZE / WRITE_SIZE with a kernel filter on the engine's
+    kernels): per leg an empty kernel (the delimiter the summary splits
+    dispatches on), then the leg's step `args.steps` times. The ceiling read
+    runs once (a read of known size: a second calibration beside the copy).
+    Prints {"counter_pass": [{leg, reps, launch_bytes}, ...]}: the algorithmic
+    bytes of each launch of one step, in dispatch order."""
+    seq = []
+
+    def run(name, leg, reps):
+        eng.empty_kernel()
+        for _ in range(reps):
+            leg.fn()
+        torch.cuda.synchronize()
+        seq.append({"leg": name, "reps": reps, "launch_bytes": leg.launch_bytes})
+        log(f"counter pass: {name} x{reps}")
+
+    run("read ceiling", ceiling, 1)
+    for name, leg in legs.items():
+        if name != "C4 stack x5":  # the stack step again
+            run(name, leg, args.steps)
+    if not args.no_extra:
+        for m in (16, 64):
+            leg, _ = gemm_stack_leg(torch, stack, m, args.steps, args.warmup)
+            run(f"gemm M={m}", leg, args.steps)
+        for label, n, k, fmt, copies, call_bytes, kernel, leg, _ in format_axis_legs(torch, eng, args.steps,
+                                                                                       args.warmup):
+            if leg.launch_bytes is not None:  # fp16 F.linear runs no engine kernel
+                run(f"axis {label} {fmt}", leg, 1)
+    print(json.dumps({"counter_pass": seq}), flush=True)
+    return 0
 
 
 # ------------------------------------------------------------ CPU baseline
@@ -638,15 +714,18 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     eng = Engine(torch)
+    Leg.eager = args.counters
     torch.backends.cuda.matmul.allow_tf32 = False
     log(f"device: {torch.cuda.get_device_name(0)}  torch {torch.__version__}")
     extra = not args.no_extra
 
     if args.calibrate_copy:
-        src = torch.empty(2 ** 28, dtype=torch.int32, device="cuda").fill_(1)
+        # a plain copy of known size for the counters: the engine's add_one
+        # kernel over 2^28 floats reads 1 GiB and writes 1 GiB
+        src = torch.ones(2 ** 28, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            eng.add_one(src, dst)
         torch.cuda.synchronize()
         log("calibration copy: 1 GiB read + 1 GiB write, 3 times")
         del src, dst
@@ -706,8 +785,13 @@ def main():
                 fused.gemv_rmsnorm(x["gate_up"], gamma, 1e-5, [layer["gate_proj"], layer["up_proj"]])
                 fused.gemv_swiglu(x["down"], ups[li], layer["down_proj"])
 
-        legs["prologue fused"] = Leg(torch, "fused", capture(torch, run_fused), args.steps, args.warmup,
-                                     legs["prologue plain"].step_bytes, layers=args.layers)
+        # the fused launches read gamma (q|k|v, gate|up) or up (down) besides
+        # the plain launches' bytes
+        extra = [3 * HIDDEN * 2, 0, 2 * HIDDEN * 2, INTER * 2]
+        legs["prologue fused"] = Leg(torch, "fused", run_fused, args.steps, args.warmup,
+                                     legs["prologue plain"].step_bytes, layers=args.layers,
+                                     launch_bytes=[b + extra[i % 4] for i, b in
+                                                   enumerate(legs["prologue plain"].launch_bytes)])
         for mode, ls in c5_launches(*c5).items():
             legs[f"C5 {mode}"] = gemv_leg(torch, eng, mode, ls, args.steps, args.warmup, C5_LAYERS)
         for name, n, k, spec, m in SINGLE_CONFIGS:
@@ -718,22 +802,25 @@ def main():
                 for p in pws:
                     eng.gemv_group([x], [p])
 
-            legs[f"single {name}"] = Leg(torch, name, capture(torch, fn), 10, 2)
+            legs[f"single {name}"] = Leg(torch, name, fn, 10, 2,
+                                         launch_bytes=[launch_bytes([x], [pws[0]])] * len(pws))
             singles_meta[name] = (n, k, spec, m, len(pws), launch_bytes([x], [pws[0]]),
                                   eng.kernel_name([x], [pws[0]])[0])
 
     def ceiling_fn():
         eng.stream_read(ceiling_buf, sink)
 
-    ceiling = Leg(torch, "read ceiling", capture(torch, ceiling_fn), CEILING_REPS, CEILING_WARM,
-                  ceiling_buf.numel() * 4)
+    ceiling = Leg(torch, "read ceiling", ceiling_fn, CEILING_REPS, CEILING_WARM, ceiling_buf.numel() * 4,
+                  launch_bytes=[ceiling_buf.numel() * 4])
 
     def empty_fn():
         for _ in range(EMPTY_LAUNCHES):
             eng.empty_kernel()
 
-    empty = Leg(torch, "empty kernels", capture(torch, empty_fn), 10, 3)
+    empty = Leg(torch, "empty kernels", empty_fn, 10, 3, launch_bytes=[0] * EMPTY_LAUNCHES)
     torch.cuda.synchronize()
+    if args.counters:
+        return counter_pass(torch, args, eng, stack, ceiling, legs)
     log(f"captured {len(legs) + 2} graphs")
 
     # ---- 3. timed legs, back to back, one synchronization at the end
@@ -869,6 +956,8 @@ def main():
         "cpu_baseline": cpu,
         "ceilings": ceilings,
         "protocol": {"build_s": build_s, "order": ["read ceiling"] + list(legs) + ["empty kernels"],
+                     "legs": {name: [len(leg.launch_bytes), leg.warmup, leg.steps] for name, leg in
+                              [("read ceiling", ceiling)] + list(legs.items()) + [("empty kernels", empty)]},
                      "note": "every input built and every graph captured before timing; nothing freed; the legs "
                              "replayed back to back with one synchronization at the end"},
         "modes": {mode: results[f"C4 {mode}"] for mode in modes},
