@@ -792,6 +792,26 @@ def main():
                                      legs["prologue plain"].step_bytes, layers=args.layers,
                                      launch_bytes=[b + extra[i % 4] for i, b in
                                                    enumerate(legs["prologue plain"].launch_bytes)])
+
+        def rmsnorm(x):  # transformers' LlamaRMSNorm in torch ops
+            h = x.float()
+            h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-5)
+            return gamma * h.to(torch.float16)
+
+        def run_unfused():
+            for li, (layer, x) in enumerate(zip(stack, xs)):
+                h = rmsnorm(x["qkv"])
+                eng.gemv_group([h] * 3, [layer["q_proj"], layer["k_proj"], layer["v_proj"]])
+                eng.gemv_group([x["o"]], [layer["o_proj"]])
+                h = rmsnorm(x["gate_up"])
+                eng.gemv_group([h] * 2, [layer["gate_proj"], layer["up_proj"]])
+                eng.gemv_group([torch.nn.functional.silu(x["down"]) * ups[li]], [layer["down_proj"]])
+
+        # what a decoder runs without the fused prologues: the same launches
+        # plus the RMSNorm and SwiGLU as torch ops (not counted in its bytes;
+        # the leg is timed last, as its kernel count per step is torch's)
+        unfused = Leg(torch, "unfused", run_unfused, args.steps, args.warmup, legs["prologue plain"].step_bytes,
+                      layers=args.layers, launch_bytes=legs["prologue plain"].launch_bytes)
         for mode, ls in c5_launches(*c5).items():
             legs[f"C5 {mode}"] = gemv_leg(torch, eng, mode, ls, args.steps, args.warmup, C5_LAYERS)
         for name, n, k, spec, m in SINGLE_CONFIGS:
@@ -806,6 +826,7 @@ def main():
                                          launch_bytes=[launch_bytes([x], [pws[0]])] * len(pws))
             singles_meta[name] = (n, k, spec, m, len(pws), launch_bytes([x], [pws[0]]),
                                   eng.kernel_name([x], [pws[0]])[0])
+        legs["prologue unfused"] = unfused
 
     def ceiling_fn():
         eng.stream_read(ceiling_buf, sink)
@@ -901,9 +922,14 @@ def main():
             log(f"stack INT4 M={m}: {r['ms_per_step']:.3f} ms/step  {r['gbs']:.1f} GB/s  "
                 f"{r['us_per_layer']:.2f} us/layer")
         prologue = {"plain": results["prologue plain"], "fused_prologues": results["prologue fused"],
-                    "bytes_per_step": legs["prologue plain"].step_bytes}
+                    "unfused_prologues": results["prologue unfused"],
+                    "bytes_per_step": legs["prologue plain"].step_bytes,
+                    "note": "plain: the decode launches alone (activations prepared); fused_prologues: RMSNorm "
+                            "(q|k|v, gate|up) and SwiGLU (down) inside the launches; unfused_prologues: the plain "
+                            "launches plus RMSNorm and SwiGLU as torch ops, what a decoder runs without the fusion"}
         log(f"decode launches: plain {prologue['plain']['us_per_layer']:.2f} us/layer, with fused prologues "
-            f"{prologue['fused_prologues']['us_per_layer']:.2f} us/layer")
+            f"{prologue['fused_prologues']['us_per_layer']:.2f} us/layer, with the prologues as torch ops "
+            f"{prologue['unfused_prologues']['us_per_layer']:.2f} us/layer")
         c5_r = {"layers": C5_LAYERS, "stack": results["C5 stack"], "decode": results["C5 decode"]}
         log(f"C5: stack {c5_r['stack']['ms_per_step']:.3f} ms/step {c5_r['stack']['gbs']:.1f} GB/s "
             f"{c5_r['stack']['us_per_layer']:.2f} us/layer; decode {c5_r['decode']['ms_per_step']:.3f} ms/step "
@@ -956,7 +982,8 @@ def main():
         "cpu_baseline": cpu,
         "ceilings": ceilings,
         "protocol": {"build_s": build_s, "order": ["read ceiling"] + list(legs) + ["empty kernels"],
-                     "legs": {name: [len(leg.launch_bytes), leg.warmup, leg.steps] for name, leg in
+                     "legs": {name: [None if name == "prologue unfused" else len(leg.launch_bytes), leg.warmup,
+                                     leg.steps] for name, leg in
                               [("read ceiling", ceiling)] + list(legs.items()) + [("empty kernels", empty)]},
                      "note": "every input built and every graph captured before timing; nothing freed; the legs "
                              "replayed back to back with one synchronization at the end"},

@@ -9,7 +9,9 @@ The timed phase opens with the streaming-read ceiling leg (its warm-up and
 timed launches of stream_read_kernel back to back); the other legs follow in
 the order bench.py records (protocol.order), each replaying its graph
 warm-up + steps times, launches_per_step dispatches per replay
-(protocol.legs). Only the timed replays are summarized. With the counter
+(protocol.legs; a leg recorded without a count, such as the one mixing torch
+ops into its step, ends the split). Only the timed replays are summarized.
+With the counter
 pass's output (dequant_project_amd.counters: <counter run>/FETCH_SIZE.json),
 each launch also gets its algorithmic bytes, hence GB/s per kernel.
 
@@ -86,6 +88,8 @@ def timed_legs(rows, protocol):
     out = OrderedDict()
     for leg in order:
         per, warm, steps = legs[leg]
+        if per is None:  # a leg whose dispatch count the benchmark does not know ends the split
+            break
         n = per * (warm + steps)
         seg = rows[i:i + n]
         if len(seg) != n:
@@ -122,7 +126,7 @@ def summarize(rows, line, counter_seq=None):
     return records
 
 
-def render(records, line, stats, command):
+def render(records, line, stats, command, unprofiled=None):
     roof = line.get("roofline", {})
     kern = roof.get("kernel", "")
     out = ["# Engine kernels in the benchmark's timed legs: kernel trace", "",
@@ -141,6 +145,10 @@ def render(records, line, stats, command):
         out.append(f"* this run's bench line (roofline.mean_launch_us, graph replay time / launches): "
                    f"{roof.get('mean_launch_us', float('nan')):.2f} us; achieved {roof.get('achieved', 0):.0f} GB/s, "
                    f"frac {roof.get('frac', 0):.4f}")
+        if unprofiled:
+            u = unprofiled["roofline"]
+            out.append(f"* the same command without the profiler, same box: mean launch {u['mean_launch_us']:.2f} us, "
+                       f"achieved {u['achieved']:.0f} GB/s, frac {u['frac']:.4f}; value {unprofiled['value']:.0f} GB/s")
         if st:
             s = st[0]
             out.append(f"* --stats over the whole run: {s['Calls']} calls, average {float(s['AverageNs']) / 1e3:.2f} us "
@@ -165,6 +173,7 @@ def main(argv=None):
     ap.add_argument("run_dir", help="directory holding trace/ (the rocprofv3 output) and bench.json")
     ap.add_argument("--bench", help="bench JSON of the traced run (default <run_dir>/bench.json)")
     ap.add_argument("--counters", help="counter-pass run directory (for bytes per launch)")
+    ap.add_argument("--unprofiled", help="bench JSON of the same command run without the profiler, to quote beside")
     ap.add_argument("--out", help="markdown summary to write")
     ap.add_argument("--command", action="append", default=[], help="command line(s) to quote in the summary")
     args = ap.parse_args(argv)
@@ -175,7 +184,8 @@ def main(argv=None):
     if args.counters:
         with open(os.path.join(args.counters, "FETCH_SIZE.json")) as fh:
             seq = json.loads([ln for ln in fh.read().splitlines() if ln.startswith("{")][-1])["counter_pass"]
-    text = render(summarize(rows, line, seq), line, stats, args.command)
+    text = render(summarize(rows, line, seq), line, stats, args.command,
+                  bench_line(args.unprofiled) if args.unprofiled else None)
     if args.out:
         with open(args.out, "w") as fh:
             fh.write(text)
