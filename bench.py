@@ -54,6 +54,10 @@ Printed: ONE JSON line on stdout (progress goes to stderr).
                    committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary of the
                    counter pass (a static figure, not measured in this run)
   ceilings         measured streaming-read ceiling and empty-kernel gap
+  read_floors      per launch structure (stack, decode, per_linear): the same
+                   launches as plain streaming reads of their bytes, i.e. what
+                   the structure would take at the read rate with its launch
+                   overheads (and the GEMV's time over it)
   cpu_baseline     the reference's CPU torch path (oracle/cpu_path.py) on the
                    host cores: C4 one layer (value), rows for C1-C5, 1 thread
   other_format_stacks / batch_stacks  the same stack step in INT8 and INT2,
@@ -339,6 +343,26 @@ def gemv_leg(torch, eng, name, launches, steps, warmup, layers):
     meta = {"launches_per_step": len(launches),
             "kernel_instances": {k: len(v) for k, v in kernel_instances(eng, launches).items()}}
     return Leg(torch, name, fn, steps, warmup, step_bytes, meta, layers, [launch_bytes(x, p) for _, x, p in launches])
+
+
+def read_floor_leg(torch, eng, name, flat, sink, sizes, steps, warmup, layers):
+    """A plain streaming read (stream_read_kernel) of each launch's
+    algorithmic bytes, in the same launch structure: consecutive regions of
+    `flat` (wrapping at its end), one read launch per GEMV launch."""
+    views, off = [], 0
+    for s in sizes:
+        n = (int(s) + 15) // 16 * 16
+        if off + n > flat.numel():
+            off = 0
+        views.append(flat[off:off + n])
+        off += n
+
+    def fn():
+        for v in views:
+            eng.stream_read(v, sink)
+
+    return Leg(torch, name, fn, steps, warmup, sum(v.numel() for v in views), layers=layers,
+               launch_bytes=[v.numel() for v in views])
 
 
 def kernel_durations(torch, eng, launches, reps):
@@ -761,6 +785,12 @@ def main():
     c4_launches = {mode: step_launches(stack, xs, mode) for mode in modes}
     legs = {f"C4 {mode}": gemv_leg(torch, eng, mode, c4_launches[mode], args.steps, args.warmup, args.layers)
             for mode in modes}
+    # the floor of each structure: a plain read of every launch's bytes
+    flat = ceiling_buf.view(torch.uint8)
+    for mode in modes:
+        legs[f"read floor {mode}"] = read_floor_leg(torch, eng, f"read floor {mode}", flat, sink,
+                                                    legs[f"C4 {mode}"].launch_bytes, args.steps, args.warmup,
+                                                    args.layers)
     # the headline's launch-duration leg: the same step five times in one
     # graph, so the per-replay launch overhead is spread over 70 launches
     legs["C4 stack x5"] = gemv_leg(torch, eng, "stack x5", c4_launches["stack"] * LAUNCH_LEG_STEPS, args.steps,
@@ -863,10 +893,15 @@ def main():
                 "empty_kernel_launches_per_graph": EMPTY_LAUNCHES}
     log(f"read ceiling {ceil_gbs:.0f} GB/s ({100 * ceil_gbs / PEAK_GBS:.1f}%), empty kernel "
         f"{ceilings['empty_kernel_us_per_launch']:.2f} us per launch in a graph")
+    read_floors = {}
     for mode in modes:
         r = results[f"C4 {mode}"]
+        f = results.pop(f"read floor {mode}")
+        read_floors[mode] = {"ms_per_step": f["ms_per_step"], "us_per_layer": f["us_per_layer"], "gbs": f["gbs"],
+                             "pct_peak": f["pct_peak"], "gemv_time_vs_floor": r["ms_per_step"] / f["ms_per_step"]}
         log(f"mode {mode}: {r['ms_per_step']:.3f} ms/step  {r['gbs']:.1f} GB/s  {r['us_per_layer']:.2f} us/layer  "
-            f"({r['launches_per_step']} launches)")
+            f"({r['launches_per_step']} launches); a plain read of the same launches {f['us_per_layer']:.2f} "
+            f"us/layer ({f['gbs']:.0f} GB/s)")
 
     # ---- 4. the headline kernel's launch duration
     # (a) live, over timed replays: the launch-duration leg replays the stack
@@ -988,6 +1023,7 @@ def main():
                      "note": "every input built and every graph captured before timing; nothing freed; the legs "
                              "replayed back to back with one synchronization at the end"},
         "modes": {mode: results[f"C4 {mode}"] for mode in modes},
+        "read_floors": read_floors,
         "other_format_stacks": other_stacks,
         "batch_stacks": batch_stacks,
         "gemm_small_stacks": gemm,
