@@ -1010,12 +1010,13 @@ struct PairStage {
 };
 
 // Thread t's word of the batch starting at column cbase (columns >= ce and a
-// batch past the walk's end load zeros).
+// batch past the walk's end load zeros): from x, or from the RMSNorm
+// prologue's gamma (same layout, one row).
 template <int BITS>
-__device__ __forceinline__ void pair_stage_issue(const KernelProblem& d, int cbase, int ce, bool live,
-                                                 uint32_t (&raw)[PairStage<BITS>::kWordDwords]) {
+__device__ __forceinline__ void pair_stage_issue(const void* base, const KernelProblem& d, int cbase, int ce,
+                                                 bool live, uint32_t (&raw)[PairStage<BITS>::kWordDwords]) {
   using PS = PairStage<BITS>;
-  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(d.K) * 2u);
+  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(base, static_cast<uint32_t>(d.K) * 2u);
   const int t = static_cast<int>(threadIdx.x);
   const int c = cbase + (t >> 2);
   const uint32_t off = live && c < ce ? static_cast<uint32_t>(c) * PS::kColumnBytes + (t & 3) * PS::kWordBytes
@@ -1031,6 +1032,20 @@ __device__ __forceinline__ void pair_stage_issue(const KernelProblem& d, int cba
 #pragma unroll
       for (int e = 0; e < 4; ++e) raw[4 * q + e] = v[e];
     }
+  }
+}
+
+// The RMSNorm prologue on a staged word: the thread's sum(x^2) in fp32 (one
+// v_dot2 per dword), then x * gamma as fp16 products (the arithmetic of
+// x_pairs_pro).
+template <int BITS>
+__device__ __forceinline__ void pair_stage_rmsnorm(uint32_t (&raw)[PairStage<BITS>::kWordDwords],
+                                                   const uint32_t (&gam)[PairStage<BITS>::kWordDwords],
+                                                   float& ssq) {
+#pragma unroll
+  for (int i = 0; i < PairStage<BITS>::kWordDwords; ++i) {
+    ssq = __builtin_amdgcn_fdot2(as_h2(raw[i]), as_h2(raw[i]), ssq, false);
+    raw[i] = __builtin_bit_cast(uint32_t, as_h2(raw[i]) * as_h2(gam[i]));
   }
 }
 
@@ -1067,14 +1082,24 @@ __device__ __forceinline__ void pair_stage_read(const unsigned char* buf, int la
   }
 }
 
-template <int BITS, bool SYM, bool INTER, int R>
+// PRO = kProRmsNorm: the staging threads apply the RMSNorm prologue to the
+// words they stage (x * gamma, and their fp32 sum(x^2) accumulated over the
+// tile's batches: every activation of the tile's K is staged once per
+// block-tile, by one thread); at the tile's end the block sums those partial
+// sums (every tile of a block-tile shares x) and each row's dot product is
+// multiplied by 1 / sqrt(sum(x^2) / K + eps) before the fp16 store.
+template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 __global__ void __launch_bounds__(kGemvThreads)
 gemv_m1_pipe_kernel(const KernelBatch b) {
+  static_assert(PRO == kProNone || PRO == kProRmsNorm, "pipelined prologue");
   using F = Fmt<BITS>;
   using PS = PairStage<BITS>;
+  constexpr bool RMS = PRO == kProRmsNorm;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   __shared__ __align__(16) unsigned char xs[2 * PS::kBufBytes];
+  __shared__ float rms_part[kWavesPerBlock];
+  float ssq = 0.f;  // RMS: this thread's sum(x^2) over the current tile's staged words
   ClassMagics<BITS> cm;
   cm.init();
   const int total = b.bt_start[b.count];
@@ -1085,17 +1110,19 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
   int cb = t.cb;
   int par = 0;
   BatchAddr<R> a;
-  uint32_t raw[PS::kWordDwords];
+  uint32_t raw[PS::kWordDwords], gam[RMS ? PS::kWordDwords : 1];
   uint32_t z[R], s[R];
   u32x4 w[R];
   // the first batch: activations staged, rows in flight
-  pair_stage_issue<BITS>(b.p[t.p], cb, t.ce, true, raw);
+  pair_stage_issue<BITS>(b.p[t.p].x, b.p[t.p], cb, t.ce, true, raw);
+  if constexpr (RMS) pair_stage_issue<BITS>(b.p[t.p].aux, b.p[t.p], cb, t.ce, true, gam);
   batch_addr<BITS, SYM, R>(b.p[t.p], t.row0, cb, t.ce, lane, t.active, a);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     issue_row<SYM, R>(a, r, z[r], s[r], w[r]);
     __builtin_amdgcn_sched_barrier(0);
   }
+  if constexpr (RMS) pair_stage_rmsnorm<BITS>(raw, gam, ssq);
   pair_stage_write<BITS, INTER>(xs, raw);
   lds_barrier();
   float yacc[R];
@@ -1124,7 +1151,8 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     if constexpr (SYM) C = __builtin_fmaf(static_cast<float>(F::BIAS), S, C);
     // the next batch's activations (issued first: vmcnt retires in order),
     // then its rows as the current ones free their registers
-    pair_stage_issue<BITS>(b.p[np], ncb, nt.ce, nvalid, raw);
+    pair_stage_issue<BITS>(b.p[np].x, b.p[np], ncb, nt.ce, nvalid, raw);
+    if constexpr (RMS) pair_stage_issue<BITS>(b.p[np].aux, b.p[np], ncb, nt.ce, nvalid, gam);
     batch_addr<BITS, SYM, R>(b.p[np], nt.row0, ncb, nt.ce, lane, nvalid && nt.active, a);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1137,6 +1165,20 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     }
     if (tile_end) {
       wave_sum_rows<R>(yacc);
+      if constexpr (RMS) {
+        // the block-tile's sum(x^2): every staging thread's partial sum of its
+        // words (computed once per block and activation vector instead, for
+        // the problems of a launch that share x, it made the decode step 0.4%
+        // faster and cost the 8-row instance a wave per SIMD)
+        float sq[1] = {ssq};
+        wave_sum_lane63<1>(sq);
+        if (lane == 63) rms_part[wave] = sq[0];
+        lds_barrier();  // every wave of the block ends its tile here
+        const float f = inv_rms(rms_part[0] + rms_part[1] + rms_part[2] + rms_part[3], b.p[t.p].K, b.eps);
+#pragma unroll
+        for (int i = 0; i < R / 4; ++i) yacc[i] *= f;
+        ssq = 0.f;
+      }
       if (t.active && (lane & 15) == 15)
         store_rows<R / 4>(b.p[t.p].y, t.row0 + (lane >> 4) * (R / 4), b.p[t.p].N, yacc);
 #pragma unroll
@@ -1144,6 +1186,7 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     }
     if (!nvalid) break;
     par ^= 1;
+    if constexpr (RMS) pair_stage_rmsnorm<BITS>(raw, gam, ssq);
     pair_stage_write<BITS, INTER>(xs + par * PS::kBufBytes, raw);
     lds_barrier();  // the other buffer was read before the previous barrier
     cb = ncb;
@@ -1171,9 +1214,9 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
 // sum is taken once per tile (DPP row_ror 4 / 8 inside 16-lane rows, then the
 // gfx950 permlane16 / permlane32 swaps across rows).
 //
-// Zero points outside [-1024, 1024] (WIDE, rare, asymmetric only): the tile
-// is recomputed with q alone for those rows and z * sum(x) subtracted in fp32,
-// sum(x) per chunk and batch row from one more MFMA chain against ones.
+// Zero points outside [-1024, 1024] (WIDE, rare, asymmetric only): those rows
+// use q alone and z * sum(x) is subtracted in fp32, sum(x) per chunk and
+// batch row from one more MFMA chain against ones.
 // Activations of one k-step for the whole block, staged in LDS: each step the
 // block loads, for each of its wk K-shares, the 16 chunks of x the step
 // covers (4*MG batch rows; one coalesced 16-byte piece per lane and load),
@@ -1224,144 +1267,6 @@ __device__ __forceinline__ void stage_write(unsigned char* buf, const u32x4 (&st
   }
 }
 
-// One tile (4 * NT rows x the wave's K-share) of the quad kernel. Every wave
-// of the block runs the same number of steps (inactive waves with no loads of
-// their own) so that all take part in the staging and its barriers.
-// `parity` selects the staging buffer of the next step; it runs on across
-// tiles, so consecutive steps of a block always alternate buffers (a tile's
-// first step must not overwrite the buffer the previous tile's last step may
-// still be reading).
-template <int BITS, bool SYM, bool INTER, int NT, int MG, int WK, bool WIDE>
-__device__ __forceinline__ void quad_tile(const KernelProblem& d, const TilePos& t, int M, int blk, int q,
-                                          uint32_t magic, unsigned char* lds, int& parity, f4 (&acc)[NT][MG],
-                                          bool& wide) {
-  using F = Fmt<BITS>;
-  using QS = QuadStage<BITS, MG, WK>;
-  constexpr int CPL = F::CPL, NF = CPL / 4;
-  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
-  const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
-  const __amdgpu_buffer_rsrc_t wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
-  const __amdgpu_buffer_rsrc_t sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row);
-  const __amdgpu_buffer_rsrc_t zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row);
-  uint32_t wrow[NT], mrow[NT];
-#pragma unroll
-  for (int g = 0; g < NT; ++g) {
-    const uint32_t n = static_cast<uint32_t>(min(t.row0 + 4 * g + q, d.N - 1));  // past N: re-read, never stored
-    wrow[g] = n * row_bytes;
-    mrow[g] = n * meta_row;
-  }
-  h2 pow_scale[F::NCLS];
-#pragma unroll
-  for (int c = 0; c < F::NCLS; ++c)
-    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
-  const int nsteps = d.per_wave >> 4;
-  for (int s = 0; s < nsteps; ++s) {
-    unsigned char* buf = lds + parity * QS::kBufBytes;
-    parity ^= 1;
-    // activations first: the LDS write below waits for them, not for the weights
-    u32x4 st[QS::kPerLane];
-    stage_issue<BITS, MG, WK>(d, M, s, st);
-    const int c = t.cb + 16 * s + blk;
-    const bool ok = t.active && c < t.ce;
-    const uint32_t gmo = ok ? group_of(d, c) * 2u : 0u;
-    uint32_t zb[NT], sb[NT];
-    u32x4 w[NT];
-#pragma unroll
-    for (int g = 0; g < NT; ++g)
-      zb[g] = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(zbuf, ok ? mrow[g] + gmo : kOutOfRange, 0, 0);
-#pragma unroll
-    for (int g = 0; g < NT; ++g)
-      sb[g] = __builtin_amdgcn_raw_buffer_load_b16(sbuf, ok ? mrow[g] + gmo : kOutOfRange, 0, 0);
-#pragma unroll
-    for (int g = 0; g < NT; ++g)
-      w[g] = __builtin_amdgcn_raw_buffer_load_b128(wbuf, ok ? wrow[g] + static_cast<uint32_t>(c) * 16u : kOutOfRange,
-                                                   0, 2);
-    __builtin_amdgcn_sched_barrier(0);  // every global load of the step is in flight before the staging waits
-    stage_write<BITS, MG, WK>(buf, st);
-    __syncthreads();
-    u32x4 xv[MG][CPL / 8];
-#pragma unroll
-    for (int mg = 0; mg < MG; ++mg)
-#pragma unroll
-      for (int k = 0; k < CPL / 8; ++k)
-        xv[mg][k] = *reinterpret_cast<const u32x4*>(buf + (t.kw * QS::kRows + 4 * mg + q) * QS::kRowBytes +
-                                                     blk * QS::kChunkBytes + 16 * k);
-    h2 xp[MG][CPL / 2];
-#pragma unroll
-    for (int mg = 0; mg < MG; ++mg) {
-      uint32_t xd[CPL / 2];
-#pragma unroll
-      for (int k = 0; k < CPL / 8; ++k)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xd[4 * k + e] = xv[mg][k][e];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp[mg] + j * F::PAIRS);
-    }
-    f4 xs[MG];
-    if constexpr (WIDE) {
-      const h2 one = splat(static_cast<_Float16>(1.0f));
-#pragma unroll
-      for (int mg = 0; mg < MG; ++mg) {
-        xs[mg] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int f = 0; f < NF; ++f)
-          xs[mg] = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xp[mg][2 * f], xp[mg][2 * f + 1]), cat2(one, one), xs[mg],
-                                                      0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < NT; ++g) {
-      _Float16 zh;
-      bool exact = true;
-      if constexpr (SYM) {
-        zh = static_cast<_Float16>(static_cast<float>(F::BIAS));
-      } else if constexpr (!WIDE) {
-        zh = __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb[g]));
-        wide |= (zb[g] & 0x7FFFu) > 0x6400u;
-      } else {
-        exact = (zb[g] & 0x7FFFu) <= 0x6400u;
-        zh = exact ? __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb[g])) : static_cast<_Float16>(0.0f);
-      }
-      const h2 zz = splat(zh);
-      h2 off[F::NCLS];
-#pragma unroll
-      for (int k = 0; k < F::NCLS; k += 2) {
-        const _Float16 b0 = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(k))));
-        const _Float16 b1 =
-            k + 1 < F::NCLS ? static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(k + 1)))) : b0;
-        const h2 both = -(h2{b0, b1} + zz);
-        off[k] = splat(both.x);
-        if (k + 1 < F::NCLS) off[k + 1] = splat(both.y);
-      }
-      h2 dq[CPL / 2];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t mp[F::PAIRS];
-        magic_pairs<BITS>(w[g][j], magic, mp);
-#pragma unroll
-        for (int i = 0; i < F::PAIRS; ++i)
-          dq[j * F::PAIRS + i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]);
-      }
-      const float sc = f16_to_f32(static_cast<uint16_t>(sb[g]));
-#pragma unroll
-      for (int mg = 0; mg < MG; ++mg) {
-        f4 D = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int f = 0; f < NF; ++f)
-          D = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xp[mg][2 * f], xp[mg][2 * f + 1]), cat2(dq[2 * f], dq[2 * f + 1]),
-                                                 D, 0, 0, 0);
-        if constexpr (WIDE) {
-          const float zf = exact ? 0.0f : f16_to_f32(static_cast<uint16_t>(zb[g]));
-#pragma unroll
-          for (int i = 0; i < 4; ++i) D[i] = __builtin_fmaf(-zf, xs[mg][i], D[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[g][mg][i] = __builtin_fmaf(sc, D[i], acc[g][mg][i]);
-      }
-    }
-  }
-}
-
 // Sum of v over the 16 lanes sharing l % 4, returned in lanes 0..15 (row 0;
 // the other rows get partial sums). The gfx950 permlane swaps exchange rows
 // with a zero operand, so one output of each swap is the moved row and the
@@ -1385,13 +1290,120 @@ __device__ __forceinline__ float quad_column_sum(float v) {
   return swap_sum32(swap_sum16(v));
 }
 
-// Persistent blocks walk block-tiles like the M = 1 kernel; a tile is 4 * NT
+// ------------------------------------------ quad kernel: the tile walk
+// Persistent blocks walk block-tiles like the M = 1 kernels; a tile is 4 * NT
 // rows and the WK waves of a tile split its chunks (in steps of 16), meeting
 // in LDS. Every problem of a launch uses WK waves per tile (the staging layout
-// holds WK K-shares).
+// holds WK K-shares). The walk keeps the next step in flight during the
+// current step's math with the same registers, as gemv_m1_pipe_kernel does
+// at M = 1: quad g of the next step (which may belong to the next tile of the
+// walk, or to another problem) is issued as soon as quad g of the current
+// step has been computed, the next step's activations are loaded before the
+// math and written to the other staging buffer after it, and the per-step
+// barrier orders LDS only (a __syncthreads would wait for the next step's
+// loads too). Measured against the same kernel with a step's loads issued
+// at the step and a __syncthreads per step: C2 at M = 4 15.3 -> 14.7 us per
+// call, the C4 stack at M = 2 / 4 / 8 unchanged (52-54 / 51 / 39% in that
+// A/B): those launches are not bound by one step's load latency.
+// Zero points outside [-1024, 1024] (asymmetric only) are handled in the
+// same pass: those rows use q alone and subtract z * sum(x), sum(x) per
+// chunk taken (one more MFMA chain against ones) only in steps where a wave
+// has such a row; every other row subtracts 0 * 0. A row's result does not
+// depend on the other rows' zero points.
+template <int NT>
+struct QuadAddr {
+  __amdgpu_buffer_rsrc_t wbuf, sbuf, zbuf;
+  uint32_t woff[NT], moff[NT];  // per lane: row and chunk column offsets, or out of range
+};
+
+template <int BITS, bool SYM, int NT>
+__device__ __forceinline__ void quad_addr(const KernelProblem& d, const TilePos& t, int s, int blk, int q, bool live,
+                                          QuadAddr<NT>& a) {
+  const uint32_t row_bytes = static_cast<uint32_t>(d.K) * BITS / 8;
+  const uint32_t meta_row = static_cast<uint32_t>(d.n_groups) * 2u;
+  a.wbuf = buffer_of(d.qweight, static_cast<uint32_t>(d.N) * row_bytes);
+  a.sbuf = buffer_of(d.scales, static_cast<uint32_t>(d.N) * meta_row);
+  a.zbuf = buffer_of(SYM ? d.scales : d.zeros, static_cast<uint32_t>(d.N) * meta_row);
+  const int c = t.cb + 16 * s + blk;
+  const bool ok = live && t.active && c < t.ce;
+  const uint32_t gmo = ok ? group_of(d, c) * 2u : 0u;
+#pragma unroll
+  for (int g = 0; g < NT; ++g) {
+    const uint32_t n = static_cast<uint32_t>(min(t.row0 + 4 * g + q, d.N - 1));  // past N: re-read, never stored
+    a.woff[g] = ok ? n * row_bytes + static_cast<uint32_t>(c) * 16u : kOutOfRange;
+    a.moff[g] = ok ? n * meta_row + gmo : kOutOfRange;
+  }
+}
+
+template <bool SYM, int NT>
+__device__ __forceinline__ void quad_issue(const QuadAddr<NT>& a, int g, uint32_t& z, uint32_t& s, u32x4& w) {
+  if constexpr (!SYM) z = __builtin_amdgcn_raw_buffer_load_b16(a.zbuf, a.moff[g], 0, 0);
+  s = __builtin_amdgcn_raw_buffer_load_b16(a.sbuf, a.moff[g], 0, 0);
+  w = __builtin_amdgcn_raw_buffer_load_b128(a.wbuf, a.woff[g], 0, 2);
+}
+
+// acc += scale * sum over the lane's chunk of x (q - z) for one quad of one
+// step; WIDE: rows whose zero point is outside [-1024, 1024] use q alone and
+// subtract z * xs (xs: sum(x) per chunk).
+template <int BITS, bool SYM, int MG, bool WIDE>
+__device__ __forceinline__ void quad_math(const u32x4& w, uint32_t zb, uint32_t sb,
+                                          const h2 (&xp)[MG][Fmt<BITS>::CPL / 2], const f4 (&xs)[MG],
+                                          const h2 (&pow_scale)[Fmt<BITS>::NCLS], uint32_t magic, f4 (&acc)[MG]) {
+  using F = Fmt<BITS>;
+  constexpr int CPL = F::CPL, NF = CPL / 4;
+  _Float16 zh;
+  bool exact = true;
+  if constexpr (SYM) {
+    zh = static_cast<_Float16>(static_cast<float>(F::BIAS));
+  } else if constexpr (!WIDE) {
+    zh = __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb));
+  } else {
+    exact = (zb & 0x7FFFu) <= 0x6400u;
+    zh = exact ? __builtin_bit_cast(_Float16, static_cast<uint16_t>(zb)) : static_cast<_Float16>(0.0f);
+  }
+  const h2 zz = splat(zh);
+  h2 off[F::NCLS];
+#pragma unroll
+  for (int k = 0; k < F::NCLS; k += 2) {
+    const _Float16 b0 = static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(k))));
+    const _Float16 b1 =
+        k + 1 < F::NCLS ? static_cast<_Float16>(static_cast<float>(1 << (10 - F::class_pow(k + 1)))) : b0;
+    const h2 both = -(h2{b0, b1} + zz);
+    off[k] = splat(both.x);
+    if (k + 1 < F::NCLS) off[k + 1] = splat(both.y);
+  }
+  h2 dq[CPL / 2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t mp[F::PAIRS];
+    magic_pairs<BITS>(w[j], magic, mp);
+#pragma unroll
+    for (int i = 0; i < F::PAIRS; ++i)
+      dq[j * F::PAIRS + i] = __builtin_elementwise_fma(as_h2(mp[i]), pow_scale[F::cls(i)], off[F::cls(i)]);
+  }
+  const float sc = f16_to_f32(static_cast<uint16_t>(sb));
+#pragma unroll
+  for (int mg = 0; mg < MG; ++mg) {
+    f4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      D = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xp[mg][2 * f], xp[mg][2 * f + 1]), cat2(dq[2 * f], dq[2 * f + 1]), D,
+                                             0, 0, 0);
+    if constexpr (WIDE) {
+      const float zf = exact ? 0.0f : f16_to_f32(static_cast<uint16_t>(zb));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) D[i] = __builtin_fmaf(-zf, xs[mg][i], D[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[mg][i] = __builtin_fmaf(sc, D[i], acc[mg][i]);
+  }
+}
+
 template <int BITS, bool SYM, bool INTER, int NT, int MG, int WK>
 __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBatch b) {
+  using F = Fmt<BITS>;
   using QS = QuadStage<BITS, MG, WK>;
+  constexpr int CPL = F::CPL, NF = CPL / 4;
   constexpr int NV = NT * MG * 4;  // outputs of one column q per tile: (g, mg, i)
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
@@ -1399,61 +1411,141 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
   __shared__ float part[2][kWavesPerBlock][NV][4];
   __shared__ __align__(16) unsigned char xlds[2 * QS::kBufBytes];
   const uint32_t magic = magic_vgpr();
+  h2 pow_scale[F::NCLS];
+#pragma unroll
+  for (int c = 0; c < F::NCLS; ++c)
+    pow_scale[c] = splat(static_cast<_Float16>(__builtin_ldexpf(1.0f, -F::class_pow(c))));
   const int total = b.bt_start[b.count];
-  int phase = 0;
-  int parity = 0;  // staging buffer of the next step
+  int bt = static_cast<int>(blockIdx.x);
+  if (bt >= total) return;  // block-uniform: the whole block leaves
   int p = 0;
-  for (int bt = blockIdx.x; bt < total; bt += gridDim.x) {
-    const TilePos t = locate(b, bt, wave, 4 * NT, p);
-    const KernelProblem& d = b.p[t.p];
-    f4 acc[NT][MG];
+  TilePos t = locate(b, bt, wave, 4 * NT, p);
+  int s = 0, par = 0, phase = 0;
+  QuadAddr<NT> a;
+  u32x4 st[QS::kPerLane];
+  uint32_t zb[NT], sb[NT];
+  u32x4 w[NT];
+  // the first step: activations staged, quads in flight
+  stage_issue<BITS, MG, WK>(b.p[t.p], b.M, s, st);
+  quad_addr<BITS, SYM, NT>(b.p[t.p], t, s, blk, q, true, a);
 #pragma unroll
-    for (int g = 0; g < NT; ++g)
+  for (int g = 0; g < NT; ++g) {
+    quad_issue<SYM, NT>(a, g, zb[g], sb[g], w[g]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  stage_write<BITS, MG, WK>(xlds, st);
+  lds_barrier();
+  f4 acc[NT][MG];
 #pragma unroll
-      for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
-    // every wave of the block, active or not, runs the steps (they stage x together)
-    bool wide = false;
-    quad_tile<BITS, SYM, INTER, NT, MG, WK, false>(d, t, b.M, blk, q, magic, xlds, parity, acc, wide);
-    if (!SYM && __syncthreads_or(wide)) {
+  for (int g = 0; g < NT; ++g)
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
+  for (;;) {
+    // the next step: the next 16 chunk columns of this tile, or the first
+    // step of the next block-tile (the same for the whole block)
+    const int nsteps = b.p[t.p].per_wave >> 4;
+    int ns = s + 1, nbt = bt, np = p;
+    TilePos nt = t;
+    const bool tile_end = ns >= nsteps;
+    if (tile_end) {
+      ns = 0;
+      nbt = bt + static_cast<int>(gridDim.x);
+      if (nbt < total) nt = locate(b, nbt, wave, 4 * NT, np);
+    }
+    const bool nvalid = nbt < total;  // block-uniform
+    // the current step's activation pairs
+    const unsigned char* buf = xlds + par * QS::kBufBytes;
+    h2 xp[MG][CPL / 2];
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg) {
+      uint32_t xd[CPL / 2];
+#pragma unroll
+      for (int k = 0; k < CPL / 8; ++k) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(buf + (t.kw * QS::kRows + 4 * mg + q) * QS::kRowBytes +
+                                                        blk * QS::kChunkBytes + 16 * k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xd[4 * k + e] = v[e];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp[mg] + j * F::PAIRS);
+    }
+    // the next step's activations, then its quads as the current ones free their registers
+    if (nvalid) stage_issue<BITS, MG, WK>(b.p[np], b.M, ns, st);
+    quad_addr<BITS, SYM, NT>(b.p[np], nt, ns, blk, q, nvalid, a);
+    __builtin_amdgcn_sched_barrier(0);
+    // zero points outside [-1024, 1024] in any of the wave's rows of this
+    // step (a wave-wide vote): sum(x) per chunk for their z * sum(x) term
+    f4 xs[MG];
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg) xs[mg] = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (!SYM) {
+      bool any = false;
+#pragma unroll
+      for (int g = 0; g < NT; ++g) any = any || (zb[g] & 0x7FFFu) > 0x6400u;
+      if (__builtin_amdgcn_ballot_w64(any) != 0) {  // wave-uniform
+        const h2 one = splat(static_cast<_Float16>(1.0f));
+#pragma unroll
+        for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+          for (int f = 0; f < NF; ++f)
+            xs[mg] = __builtin_amdgcn_mfma_f32_4x4x4f16(cat2(xp[mg][2 * f], xp[mg][2 * f + 1]), cat2(one, one),
+                                                        xs[mg], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < NT; ++g) {
+      quad_math<BITS, SYM, MG, !SYM>(w[g], zb[g], sb[g], xp, xs, pow_scale, magic, acc[g]);
+      quad_issue<SYM, NT>(a, g, zb[g], sb[g], w[g]);  // quad g of the next step, into the freed registers
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (tile_end) {
+      float tot[NV];
+#pragma unroll
+      for (int g = 0; g < NT; ++g)
+#pragma unroll
+        for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) tot[(g * MG + mg) * 4 + i] = quad_column_sum(acc[g][mg][i]);
+      const KernelProblem& d = b.p[t.p];
+      // value v = (g, mg, i) is y[4 mg + i][row0 + 4 g + q]; lane (b = v % 4, q) of row 0 stores it
+      if (t.wk == 1) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          const int g = v / (MG * 4), m = 4 * ((v / 4) % MG) + (v % 4), n = t.row0 + 4 * g + q;
+          if (blk == (v & 3) && t.active && m < b.M && n < d.N)
+            d.y[static_cast<int64_t>(m) * d.ldy + n] = f32_to_f16_rn(tot[v]);
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+          if (blk == (v & 3)) part[phase][wave][v][q] = tot[v];
+        lds_barrier();  // all 4 waves of the block run the same step sequence
+        if (t.active && t.kw == 0) {
+#pragma unroll
+          for (int v = 0; v < NV; ++v) {
+            const int g = v / (MG * 4), m = 4 * ((v / 4) % MG) + (v % 4), n = t.row0 + 4 * g + q;
+            if (blk == (v & 3) && m < b.M && n < d.N) {
+              float sum = 0.f;
+              for (int j = 0; j < t.wk; ++j) sum += part[phase][wave + j][v][q];
+              d.y[static_cast<int64_t>(m) * d.ldy + n] = f32_to_f16_rn(sum);
+            }
+          }
+        }
+        phase ^= 1;
+      }
 #pragma unroll
       for (int g = 0; g < NT; ++g)
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg) acc[g][mg] = f4{0.f, 0.f, 0.f, 0.f};
-      quad_tile<BITS, SYM, INTER, NT, MG, WK, true>(d, t, b.M, blk, q, magic, xlds, parity, acc, wide);
     }
-    float tot[NV];
-#pragma unroll
-    for (int g = 0; g < NT; ++g)
-#pragma unroll
-      for (int mg = 0; mg < MG; ++mg)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) tot[(g * MG + mg) * 4 + i] = quad_column_sum(acc[g][mg][i]);
-    // value v = (g, mg, i) is y[4 mg + i][row0 + 4 g + q]; lane (b = v % 4, q) of row 0 stores it
-    if (t.wk == 1) {
-#pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        const int g = v / (MG * 4), m = 4 * ((v / 4) % MG) + (v % 4), n = t.row0 + 4 * g + q;
-        if (blk == (v & 3) && t.active && m < b.M && n < d.N)
-          d.y[static_cast<int64_t>(m) * d.ldy + n] = f32_to_f16_rn(tot[v]);
-      }
-    } else {
-#pragma unroll
-      for (int v = 0; v < NV; ++v)
-        if (blk == (v & 3)) part[phase][wave][v][q] = tot[v];
-      __syncthreads();  // all 4 waves of the block run the same block-tile sequence
-      if (t.active && t.kw == 0) {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          const int g = v / (MG * 4), m = 4 * ((v / 4) % MG) + (v % 4), n = t.row0 + 4 * g + q;
-          if (blk == (v & 3) && m < b.M && n < d.N) {
-            float s = 0.f;
-            for (int j = 0; j < t.wk; ++j) s += part[phase][wave + j][v][q];
-            d.y[static_cast<int64_t>(m) * d.ldy + n] = f32_to_f16_rn(s);
-          }
-        }
-      }
-      phase ^= 1;
-    }
+    if (!nvalid) break;
+    par ^= 1;
+    stage_write<BITS, MG, WK>(xlds + par * QS::kBufBytes, st);
+    lds_barrier();  // the other buffer was read before the previous barrier
+    s = ns;
+    bt = nbt;
+    p = np;
+    t = nt;
   }
 }
 
@@ -2165,8 +2257,9 @@ constexpr bool m1_keeps_x(int bits) { return bits == 2; }
 constexpr int kKeepRun = 3;
 constexpr int kKeepRounds = 2;
 
-// Which M = 1 kernel variant a launch runs (PRO = none; prologue launches
-// always take gemv_m1_kernel's load variant):
+// Which M = 1 kernel variant a launch runs (PRO = none; of the prologue
+// launches, RMSNorm ones of one-wave tiles take gemv_m1_pipe_kernel with the
+// prologue, the others gemv_m1_kernel's load variant):
 //   kM1Stage  INT2, activations staged per block (conditions above), needs
 //             at least xl_rounds(R) rounds of its grid;
 //   kM1Keep   INT2, 8-row one-batch tiles, activations kept across tiles,
@@ -2229,6 +2322,14 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
       }
       default:
         break;
+    }
+  }
+  if constexpr (PRO == kProRmsNorm && !m1_uses_mfma(BITS)) {
+    bool one_wave = true;
+    for (int i = 0; i < count; ++i) one_wave = one_wave && wks[i] == 1;
+    if (one_wave) {
+      constexpr auto kernel = gemv_m1_pipe_kernel<BITS, SYM, INTER, R, kProRmsNorm>;
+      return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
     }
   }
   constexpr auto kernel = gemv_m1_kernel<BITS, SYM, INTER, R, m1_uses_mfma(BITS), PRO, kXmLoad>;
@@ -2417,9 +2518,19 @@ hipError_t launch_gemv_prologue_t(const GemvOperand* ops, int count, int64_t M, 
   for (int i = 0; i < count; ++i) tiles8 += (ops[i].N + 7) / 8;
   const bool wide_tiles =
       rows_per_tile(ops, count) == 8 || prologue == kPrologueSwiGlu || tiles8 >= kProWideTiles;
-  if (prologue == kPrologueRmsNorm)
-    return wide_tiles ? launch_gemv_m1<BITS, SYM, INTER, 8, kProRmsNorm>(ops, count, M, stream, eps)
-                      : launch_gemv_m1<BITS, SYM, INTER, 4, kProRmsNorm>(ops, count, M, stream, eps);
+  if (prologue == kPrologueRmsNorm) {
+    // RMSNorm launches whose 4-row tiles are one wave wide (the decode step's
+    // gate | up) keep the plain rule: launch_gemv_m1 runs them on the
+    // pipelined kernel, which applies the prologue once per block and batch.
+    // Measured on the Llama-3-8B decode gate | up launch: 14.1 us with 8-row
+    // tiles (split-K, gemv_m1_kernel) against 12.3 us for the plain launch.
+    int wks[kMaxBatch];
+    waves_per_tile(ops, count, BITS, 4, wks);
+    bool one_wave = rows_per_tile(ops, count) == 4;
+    for (int i = 0; i < count; ++i) one_wave = one_wave && wks[i] == 1;
+    return wide_tiles && !one_wave ? launch_gemv_m1<BITS, SYM, INTER, 8, kProRmsNorm>(ops, count, M, stream, eps)
+                                   : launch_gemv_m1<BITS, SYM, INTER, 4, kProRmsNorm>(ops, count, M, stream, eps);
+  }
   if (prologue == kPrologueSwiGlu)
     return wide_tiles ? launch_gemv_m1<BITS, SYM, INTER, 8, kProSwiGlu>(ops, count, M, stream)
                       : launch_gemv_m1<BITS, SYM, INTER, 4, kProSwiGlu>(ops, count, M, stream);

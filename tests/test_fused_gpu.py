@@ -50,8 +50,10 @@ def packed_group(torch, n, k, count, fmt, seed):
 
 
 # (N, K, problems): split-K tiles (one small problem) and full-K tiles (a
-# 16-problem launch), K = 11008 (172 INT2 chunks: a ragged last column)
-SHAPES = [(256, 4096, 1), (1000, 2048, 3), (4096, 4096, 16), (300, 11008, 2)]
+# 16-problem launch), K = 11008 (172 INT2 chunks: a ragged last column), and
+# two problems of one-wave 4-row tiles (the decode step's gate | up shape
+# class: RMSNorm on the pipelined kernel, the prologue staged per block)
+SHAPES = [(256, 4096, 1), (1000, 2048, 3), (4096, 4096, 16), (300, 11008, 2), (12288, 1024, 2)]
 
 
 @pytest.mark.parametrize("n,k,count", SHAPES)
