@@ -2125,8 +2125,8 @@ int rows_per_tile(const GemvOperand* ops, int count) {
 }
 
 // wk[i] for every problem of the launch (rows per tile R).
-void waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk) {
-  const int64_t target = target_waves(bits);
+void waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk, int64_t target = 0) {
+  if (target == 0) target = target_waves(bits);
   int w = 1;
   for (; w < 4; w *= 2) {
     int64_t waves = 0;
@@ -2346,9 +2346,15 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
 // operands held M = 8 to two waves per SIMD; one quad lost 4-17%).
 constexpr int kQuadsPerTile = 2;
 
+// The quad kernel's INT8 launches want fewer K-shares than the M = 1 rule
+// gives them (its waves carry M rows of MFMA work per weight): a target of
+// 2048 waves took C2 at M = 4 (11008 x 4096, per-channel) from 14.5 to 13.2-13.5
+// us per call; the same target for the M = 1 kernel cost C2 at M = 1 10%.
+int64_t quad_target_waves(int bits) { return bits == 8 ? 2048 : target_waves(bits); }
+
 int quad_waves_per_tile(const GemvOperand* ops, int count, int bits, int mg) {
   int wks[kMaxBatch];
-  waves_per_tile(ops, count, bits, 4 * kQuadsPerTile, wks);
+  waves_per_tile(ops, count, bits, 4 * kQuadsPerTile, wks, quad_target_waves(bits));
   int wk = 4;
   for (int i = 0; i < count; ++i) wk = std::min(wk, wks[i]);
   if (bits == 2 && mg == 2) wk = std::min(wk, 2);

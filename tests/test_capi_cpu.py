@@ -231,7 +231,7 @@ def test_gemv_plan_geometry():
     # 8-row tiles (two quads), wk by the M = 1 rule for 8-row tiles.
     assert plan([(4096, 4096)], m=4) == ([2], 8, 1)
     assert plan([(14336, 4096)] * 2, m=8) == ([2, 2], 8, 1)
-    assert plan([(11008, 4096)], m=4, bits=8, gs=None) == ([4], 8, 1)
+    assert plan([(11008, 4096)], m=4, bits=8, gs=None) == ([2], 8, 1)  # INT8 quad launches: 2048 waves
     assert plan([(4096, 11008)], m=4, bits=2, gs=64) == ([4], 8, 1)
     assert plan([(4096, 4096)], m=2, gs=64) == ([2], 8, 1)
     assert plan([(14336, 4096)] * 16, m=2) == ([1] * 16, 8, 1)
