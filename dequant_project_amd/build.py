@@ -70,6 +70,10 @@ def build_torch_ext():
     incs = ce.include_paths(device_type="cuda")
     libdirs = ce.library_paths(device_type="cuda")
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    # the check torch's own extension builder makes of the host compiler
+    compatible, version = ce.get_compiler_abi_compatibility_and_version("g++")
+    if not compatible:
+        raise RuntimeError(f"g++ {version} is not ABI-compatible with this torch build")
     out = PKG / ext_filename()
     tmp = out.with_suffix(".tmp")
     cmd = [

@@ -62,6 +62,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "dq_internal.h"
 
@@ -2167,24 +2168,34 @@ hipError_t launch_kernel(Kernel kernel, int blocks, const Batch& kb, hipStream_t
 }
 
 // Co-resident blocks of a kernel instance on the current device. Queried once
-// per instance: the cache is keyed by the kernel itself (a template argument),
-// because every instance of one kernel template has the same function type.
-// The engine targets a single device model, the MI355X.
+// per instance and device: the cache is keyed by the kernel itself (a
+// template argument, because every instance of one kernel template has the
+// same function type) and indexed by the device, each entry written once with
+// an atomic store (concurrent first calls on one device store the same value).
+constexpr int kMaxDevices = 64;
+
 template <auto Kernel, int THREADS = kGemvThreads>
 int resident_blocks() {
-  static int cached = 0;
-  if (cached == 0) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, THREADS, 0) != hipSuccess || cus <= 0 ||
-        per_cu <= 0) {
-      (void)hipGetLastError();
-      return 512;
-    }
-    cached = cus * per_cu;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 512;
   }
-  return cached;
+  const bool indexed = dev >= 0 && dev < kMaxDevices;
+  if (indexed) {
+    const int v = cached[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, THREADS, 0) != hipSuccess || cus <= 0 ||
+      per_cu <= 0) {
+    (void)hipGetLastError();
+    return 512;
+  }
+  if (indexed) cached[dev].store(cus * per_cu, std::memory_order_relaxed);
+  return cus * per_cu;
 }
 
 // The launch description of a list of problems cut into tiles of R rows
