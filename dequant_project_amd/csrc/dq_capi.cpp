@@ -14,8 +14,11 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <sstream>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "dequant_hip.h"
@@ -246,6 +249,40 @@ int launch_status(hipError_t e) {
   return fail(DQ_ERR_LAUNCH, cat("HIP launch failed: ", hipGetErrorString(e)));
 }
 
+// Scratch of the small GEMM's split along K (dq::kGemmScratchBytes), one per
+// device and stream, so that launches on different streams never share one:
+// allocated on the stream's first dq_gemm_small with 16 < M and kept until
+// the process ends. A stream first seen inside a graph capture gets its
+// scratch too: the thread's capture mode is relaxed for the allocation, as
+// torch's allocator does (the scratch needs no initial contents). If that
+// fails the stream gets none and its launches run unsplit, with the same
+// results.
+void* gemm_scratch(hipStream_t stream) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, void*> table;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, stream);
+  const auto it = table.find(key);
+  if (it != table.end()) return it->second;
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  void* p = nullptr;
+  const bool ok = hipMalloc(&p, dq::kGemmScratchBytes) == hipSuccess;
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  (void)hipGetLastError();
+  if (!ok) return nullptr;
+  table.emplace(key, p);
+  return p;
+}
+
 }  // namespace
 
 extern "C" {
@@ -433,9 +470,10 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
                                bits, ops);
   }
   if (ops.empty()) return DQ_OK;
+  const hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  void* scratch = gemm_scratch(hs);
   return launch_status(launch_in_groups(ops, [&](const dq::GemvOperand* o, int n) {
-    return dq::launch_gemm_batch(o, n, M, static_cast<int>(bits), symmetric != 0, interleaved != 0,
-                                 reinterpret_cast<hipStream_t>(stream));
+    return dq::launch_gemm_batch(o, n, M, static_cast<int>(bits), symmetric != 0, interleaved != 0, scratch, hs);
   }));
 }
 

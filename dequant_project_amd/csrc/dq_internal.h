@@ -55,12 +55,18 @@ hipError_t launch_gemv_prologue_batch(const GemvOperand* ops, int count, int64_t
 // Largest M the small fused GEMM takes (launch_gemm_batch).
 constexpr int kMaxGemmM = 64;
 
+// Scratch of the small GEMM's split along K (launch_gemm_batch): fp32
+// partial tiles, written by one launch and summed by the next. Launches that
+// share one scratch must not overlap.
+constexpr int64_t kGemmScratchBytes = int64_t(8) << 20;
+
 // y = x @ W16^T for 1 <= M <= kMaxGemmM with W16 the fp16 weight that
 // dequantize materializes, built in registers (one pass over the packed
 // bytes, fp32 accumulation on the matrix cores). Same operands as
-// launch_gemv_batch.
+// launch_gemv_batch. `scratch` (kGemmScratchBytes, or null: no split along
+// K) serves launches with 16 < M.
 hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
-                             bool interleaved, hipStream_t stream);
+                             bool interleaved, void* scratch, hipStream_t stream);
 
 struct DequantProblem {
   const uint32_t* qweight;

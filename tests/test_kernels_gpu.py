@@ -288,11 +288,12 @@ def check_gemm_small(torch, pw, qw, sc, ze, ms, label):
 @pytest.mark.parametrize("fmt", [(4, 128, False, "sequential"), (4, 64, True, "interleaved"),
                                  (8, None, True, "sequential")])
 def test_gemm_small_shared_activation_kernel(torch_gpu, fmt):
-    """gemm_small at M <= 32 on a gate_proj shape (14336 x 4096: 896 tiles of
-    16 rows, split 4 ways along K), which runs the variant that shares each
-    K-share's activations across the block's tiles (M <= 16: 4 tiles, 224
-    blocks of 16 waves; M <= 32: 2 tiles, 448 blocks of 8 waves), against
-    the dequantized product on a sample of rows including the last tile."""
+    """gemm_small on a gate_proj shape (14336 x 4096) at M <= 32: M <= 16 runs
+    the variant that shares each K-share's activations across the block's 4
+    tiles (896 tiles of 16 rows split 4 ways along K, 224 blocks of 16
+    waves), 16 < M <= 32 the column walk (224 groups of 64 columns, unsplit),
+    against the dequantized product on a sample of rows including the last
+    tile."""
     torch = torch_gpu
     from dequant_project_amd.packer import QuantConfig, quantize_tensor
 
@@ -377,6 +378,34 @@ def test_gemm_small_zero_points_beyond_fp16_exact_range(torch_gpu):
         pw, qw, sc, ze = pack_on_gpu(torch, w.astype(np.float16), *fmt)
         assert (np.abs(ze.astype(np.float32)[band]) > 1024).all()
         check_gemm_small(torch, pw, qw, sc, ze, (12, 40), f"gemm_small wide zeros {fmt}")
+
+
+def test_gemm_small_split_along_k_in_graph_replays(torch_gpu):
+    """16 < M <= 64 launches with few column groups split K across blocks:
+    partial tiles in a per-stream scratch, summed in split order by a second
+    launch. Captured in a CUDA graph on a stream that never ran a small GEMM
+    (its scratch is allocated inside the capture), every replay, with eager
+    work and synchronizations between them, must equal the eager result
+    bit for bit; the eager result passes the dequantized-product check."""
+    torch = torch_gpu
+    n, k = 1000, 4096  # 16 column groups: 8 splits of 4 iterations
+    pw, qw, sc, ze = pack_on_gpu(torch, gauss_weight(n, k, seed=91), 4, 128, False, "sequential")
+    for m in (40, 64):
+        check_gemm_small(torch, pw, qw, sc, ze, (m,), f"split gemm_small [{n},{k}]")
+        x = to_gpu(torch, activations(m, k, seed=100 + m))
+        eager = ext().gemm_small(x, *ext_args(pw))
+        y = torch.empty_like(eager)
+        side = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            y.copy_(ext().gemm_small(x, *ext_args(pw)))
+        for rep in range(3):
+            y.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, eager), f"M={m} replay {rep} differs from the eager result"
+            ext().gemm_small(x * 2, *ext_args(pw))  # eager work on the default stream between replays
+            torch.cuda.synchronize()
 
 
 def test_gemm_small_rejects_batches_past_its_range(torch_gpu):
