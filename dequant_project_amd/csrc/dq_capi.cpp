@@ -283,6 +283,42 @@ void* gemm_scratch(hipStream_t stream) {
   return p;
 }
 
+// dq_gemm_small and dq_gemm_small_noalloc: the same validation and kernels;
+// the split scratch comes from the per-stream table (allocated on first use)
+// or, allocating nothing, from the library's static per-device array.
+int gemm_small_call(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
+                    int interleaved, dq_stream_t stream, bool noalloc) {
+  g_error.clear();
+  if (count < 1 || count > DQ_MAX_BATCH)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("count must be in [1, ", DQ_MAX_BATCH, "], got ", count));
+  if (!problems) return fail(DQ_ERR_INVALID_ARGUMENT, "problems must not be NULL");
+  int st = check_gemm_m(M);
+  if (st) return st;
+  std::vector<dq::GemvOperand> ops;
+  for (int i = 0; i < count; ++i) {
+    const dq_gemv_problem& p = problems[i];
+    if ((st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, M, p.N, p.K, bits, p.group_size,
+                                 symmetric))) {
+      g_error = cat("problem ", i, ": ", g_error);
+      return st;
+    }
+    if (p.N > 0) append_slices(dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size},
+                               bits, ops);
+  }
+  if (ops.empty()) return DQ_OK;
+  const hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  void* scratch = nullptr;
+  if (!noalloc) {
+    scratch = gemm_scratch(hs);
+  } else if (const hipError_t e = dq::gemm_static_scratch(&scratch); e != hipSuccess) {
+    return fail(DQ_ERR_HIP, cat("gemm_small_noalloc: no address for the static scratch on this device: ",
+                                hipGetErrorString(e)));
+  }
+  return launch_status(launch_in_groups(ops, [&](const dq::GemvOperand* o, int n) {
+    return dq::launch_gemm_batch(o, n, M, static_cast<int>(bits), symmetric != 0, interleaved != 0, scratch, hs);
+  }));
+}
+
 }  // namespace
 
 extern "C" {
@@ -452,29 +488,12 @@ int dq_gemv_prologue_batched(const dq_gemv_problem* problems, const void* const*
 
 int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
                   int interleaved, dq_stream_t stream) {
-  g_error.clear();
-  if (count < 1 || count > DQ_MAX_BATCH)
-    return fail(DQ_ERR_INVALID_ARGUMENT, cat("count must be in [1, ", DQ_MAX_BATCH, "], got ", count));
-  if (!problems) return fail(DQ_ERR_INVALID_ARGUMENT, "problems must not be NULL");
-  int st = check_gemm_m(M);
-  if (st) return st;
-  std::vector<dq::GemvOperand> ops;
-  for (int i = 0; i < count; ++i) {
-    const dq_gemv_problem& p = problems[i];
-    if ((st = check_gemv_problem(p.x, p.qweight, p.scales, p.zeros, p.y, M, p.N, p.K, bits, p.group_size,
-                                 symmetric))) {
-      g_error = cat("problem ", i, ": ", g_error);
-      return st;
-    }
-    if (p.N > 0) append_slices(dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size},
-                               bits, ops);
-  }
-  if (ops.empty()) return DQ_OK;
-  const hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
-  void* scratch = gemm_scratch(hs);
-  return launch_status(launch_in_groups(ops, [&](const dq::GemvOperand* o, int n) {
-    return dq::launch_gemm_batch(o, n, M, static_cast<int>(bits), symmetric != 0, interleaved != 0, scratch, hs);
-  }));
+  return gemm_small_call(problems, count, M, bits, symmetric, interleaved, stream, false);
+}
+
+int dq_gemm_small_noalloc(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
+                          int interleaved, dq_stream_t stream) {
+  return gemm_small_call(problems, count, M, bits, symmetric, interleaved, stream, true);
 }
 
 int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* waves_per_tile,

@@ -68,6 +68,10 @@ constexpr int64_t kGemmScratchBytes = int64_t(8) << 20;
 hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
                              bool interleaved, void* scratch, hipStream_t stream);
 
+// Device address, on the current device, of the library's static scratch
+// (kGemmScratchBytes) for dq_gemm_small_noalloc; allocates nothing.
+hipError_t gemm_static_scratch(void** out);
+
 struct DequantProblem {
   const uint32_t* qweight;
   const uint16_t* scales;

@@ -63,6 +63,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 #include "dq_internal.h"
 
@@ -2988,6 +2989,34 @@ hipError_t launch_gemv_prologue_batch(const GemvOperand* ops, int count, int64_t
 #define DQ_CALL_PRO(B, S, I) launch_gemv_prologue_t<B, S, I>(ops, count, M, prologue, eps, stream)
   DQ_DISPATCH_12(bits, symmetric, interleaved, DQ_CALL_PRO)
 #undef DQ_CALL_PRO
+}
+
+// Scratch of dq_gemm_small_noalloc, for callers that cannot allocate: the
+// small GEMM's split partial tiles in a static device array, one per GPU,
+// held until the process ends. Host code never passes the array's name to a
+// kernel (on the host it stands for no device address): its address on each
+// device comes from hipGetSymbolAddress, taken once per device with that
+// device current, and every launch gets that pointer. Nothing in it needs
+// initial contents (a launch writes each partial tile before the next launch
+// reads it); launches that use it and overlap on one GPU race.
+static __device__ __align__(256) unsigned char scratch[kGemmScratchBytes];
+
+hipError_t gemm_static_scratch(void** out) {
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,

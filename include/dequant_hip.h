@@ -202,6 +202,20 @@ int dq_gemv_prologue_batched(const dq_gemv_problem* problems, const void* const*
 int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
                   int interleaved, dq_stream_t stream);
 
+/* dq_gemm_small for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc); no
+ * counterpart in the reference. Same operands, kernels and results as
+ * dq_gemm_small, which allocates an 8 MiB scratch per stream on first use
+ * for the split along K of launches with 16 < M; this entry point allocates
+ * nothing: it uses the library's static 8 MiB device array, one per GPU,
+ * held until the process ends. A launch plans its split within that array
+ * (one needing more partial tiles takes fewer splits, down to none), so no
+ * size exceeds it; M past DQ_MAX_GEMM_M is rejected as by dq_gemm_small.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (on different streams) race. */
+int dq_gemm_small_noalloc(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
+                          int interleaved, dq_stream_t stream);
+
 /* Geometry the launch of these problems would use (no reference
  * counterpart), for profiling and tuning tools; pure host logic. For each
  * problem i, waves_per_tile[i] waves (1, 2 or 4) share one tile along K;
