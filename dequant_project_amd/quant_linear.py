@@ -37,22 +37,22 @@ MAX_M = 8
 MAX_M_GEMM = 64
 
 # Measured on MI355X against dequantize + F.linear over the Llama-3-8B
-# projection shapes: the fused small GEMM is 1.2-3.7x faster up to 32 rows;
-# at 33..64 rows it still wins on weights of up to 2^25 codes (1.3x at
-# 4096 x 4096) but not beyond (0.7x at 14336 x 4096, 1.0x at 4096 x 14336).
-GEMM_SMALL_MAX_CODES_ABOVE_32 = 1 << 25
+# projection shapes: the fused small GEMM is faster at every batch of 9..64
+# rows, at 33..64 rows by 1.5-2.4x across INT4 / INT8 / INT2 formats on the
+# 4096 x 4096, 14336 x 4096 and 4096 x 14336 weights (the column walk), so
+# the whole range takes it.
 
 
 def uses_gemm_small(m, n, k, cfg=None, x=None):
     """Whether QuantLinear runs the fused small GEMM for m rows of an [n, k] weight.
 
-    Besides the measured size rule, the small GEMM takes the GEMV kernels'
-    operand rules: group_size a multiple of 128/bits codes (one 16-byte
-    chunk per group at least; INT2 g32 is excluded) and x 16-byte aligned.
-    Inputs outside them take the reference's dequantize + F.linear path,
-    which has neither restriction.
+    Batches of 9..64 rows take it under the GEMV kernels' operand rules:
+    group_size a multiple of 128/bits codes (one 16-byte chunk per group at
+    least; INT2 g32 is excluded) and x 16-byte aligned. Inputs outside them
+    take the reference's dequantize + F.linear path, which has neither
+    restriction.
     """
-    if not (MAX_M < m <= MAX_M_GEMM and (m <= 32 or n * k <= GEMM_SMALL_MAX_CODES_ABOVE_32)):
+    if not MAX_M < m <= MAX_M_GEMM:
         return False
     if cfg is not None and cfg.effective_group_size(k) % (128 // cfg.bits) != 0:
         return False

@@ -193,6 +193,8 @@ def test_gemm_small_routing_respects_operand_rules():
     assert uses_gemm_small(48, 1024, 3072, QuantConfig(2, 64, True))
     assert not uses_gemm_small(8, 1024, 3072, QuantConfig(4, 128, False))      # the GEMV's range
     assert not uses_gemm_small(65, 1024, 3072, QuantConfig(4, 128, False))
+    assert uses_gemm_small(64, 14336, 4096, QuantConfig(4, 128, False))          # large weights too
+    assert uses_gemm_small(40, 4096, 14336, QuantConfig(8, None, True))
     x = torch.zeros(16 * 3072 + 1, dtype=torch.float16)[1:].view(16, 3072)     # 2-byte offset
     assert not uses_gemm_small(16, 1024, 3072, QuantConfig(4, 128, False), x)
 
