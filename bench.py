@@ -490,6 +490,30 @@ def single_copies(torch, n, k, cfg, seed, outliers=False):
                       for _ in range(copies - 1)]
 
 
+GEMM_MS = (16, 32, 64)  # batch rows of the small-GEMM legs
+
+
+def gemm_dispatch_bytes(x, p):
+    """Algorithmic bytes of each kernel launch of one gemm_small call, in
+    launch order: one launch, or, for a call the engine splits along K
+    (dq_gemm_small_plan), the walk (weights, scales, zeros, activations) and
+    the launch that sums its partial tiles (the output; the partials it reads
+    are traffic beyond the algorithmic bytes)."""
+    from dequant_project_amd import _native
+
+    lib = _native.capi()
+    pr = _native.DqGemvProblem()
+    pr.N, pr.K = p.shape
+    pr.group_size = p.config.effective_group_size(p.shape[1])
+    splits = (ctypes.c_int * 1)()
+    _native.check(lib.dq_gemm_small_plan(ctypes.byref(pr), 1, x.shape[0], p.config.bits, splits))
+    total = launch_bytes([x], [p])
+    if splits[0] == 1:
+        return [total]
+    out = x.shape[0] * p.shape[0] * 2
+    return [total - out, out]
+
+
 def gemm_stack_leg(torch, stack, m, steps, warmup):
     """The fused small GEMM (quant_linear.gemm_small) over every projection of
     the stack at m rows (a prefill chunk through all layers) as one leg, and
@@ -499,7 +523,7 @@ def gemm_stack_leg(torch, stack, m, steps, warmup):
     gen = torch.Generator(device="cuda").manual_seed(20251204 + m)
     xs = {k: torch.randn(m, k, generator=gen, device="cuda", dtype=torch.float16) for k in (HIDDEN, INTER)}
     items = [(xs[p.shape[1]], p) for layer in stack for _, p in sorted(layer.items())]
-    per_launch = [launch_bytes([x], [p]) for x, p in items]
+    per_launch = [b for x, p in items for b in gemm_dispatch_bytes(x, p)]
 
     def fused():
         for x, p in items:
@@ -640,7 +664,7 @@ def counter_pass(torch, args, eng, stack, ceiling, legs):
         if name != "C4 stack x5":  # the stack step again
             run(name, leg, args.steps)
     if not args.no_extra:
-        for m in (16, 64):
+        for m in GEMM_MS:
             leg, _ = gemm_stack_leg(torch, stack, m, args.steps, args.warmup)
             run(f"gemm M={m}", leg, args.steps)
         for label, n, k, fmt, copies, call_bytes, kernel, leg, _ in format_axis_legs(torch, eng, args.steps,
@@ -982,7 +1006,7 @@ def main():
     # ---- 5. legs that build and time in place (their builds reuse cached memory)
     gemm, axis = {}, []
     if extra:
-        for m in (16, 64):
+        for m in GEMM_MS:
             g = gemm[f"M={m}"] = gemm_stack(torch, stack, m, args.steps, args.warmup)
             log(f"gemm_small stack M={m}: {g['ms_per_step']:.3f} ms/step  {g['gbs']:.1f} GB/s  "
                 f"(dequantize + F.linear {g['dequantize_plus_linear_ms_per_step']:.3f} ms/step, "

@@ -89,6 +89,7 @@ SIGNATURES = {
     "dq_gemv_batched": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, _I, _I, _P]),
     "dq_gemm_small": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, _I, _I, _P]),
     "dq_gemm_small_noalloc": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, _I, _I, _P]),
+    "dq_gemm_small_plan": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, ctypes.POINTER(ctypes.c_int)]),
     "dq_gemv_prologue_batched": (_I, [ctypes.POINTER(DqGemvProblem), ctypes.POINTER(_P), _I, _I64, _I64, _I, _I,
                                       _I, ctypes.c_float, _P]),
     "dq_gemv_plan": (_I, [ctypes.POINTER(DqGemvProblem), _I, _I64, _I64, ctypes.POINTER(ctypes.c_int),

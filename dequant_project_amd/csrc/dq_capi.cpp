@@ -496,6 +496,28 @@ int dq_gemm_small_noalloc(const dq_gemv_problem* problems, int count, int64_t M,
   return gemm_small_call(problems, count, M, bits, symmetric, interleaved, stream, true);
 }
 
+int dq_gemm_small_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* splits) {
+  g_error.clear();
+  if (count < 1 || count > DQ_MAX_BATCH)
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("count must be in [1, ", DQ_MAX_BATCH, "], got ", count));
+  if (!problems || !splits) return fail(DQ_ERR_INVALID_ARGUMENT, "problems and splits must not be NULL");
+  int st = check_gemm_m(M);
+  if (st) return st;
+  if (!(bits == 2 || bits == 4 || bits == 8))
+    return fail(DQ_ERR_INVALID_ARGUMENT, cat("bits must be 2, 4 or 8, got ", bits));
+  dq::GemvOperand ops[DQ_MAX_BATCH];
+  for (int i = 0; i < count; ++i) {
+    const dq_gemv_problem& p = problems[i];
+    if (p.K <= 0 || p.K % (128 / bits) != 0 || p.N < 0)
+      return fail(DQ_ERR_INVALID_ARGUMENT, cat("problem ", i, ": K=", p.K, " must be a positive multiple of ",
+                                               128 / bits, " and N=", p.N, " non-negative"));
+    ops[i] = dq::GemvOperand{p.x, p.qweight, p.scales, p.zeros, p.y, p.N, p.K, p.group_size};
+  }
+  const int S = dq::gemm_walk_splits(ops, count, M, static_cast<int>(bits), true);
+  for (int i = 0; i < count; ++i) splits[i] = S == 1 ? 1 : dq::gemm_problem_splits(ops[i].K, static_cast<int>(bits), S);
+  return DQ_OK;
+}
+
 int dq_gemv_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* waves_per_tile,
                  int* rows_per_tile, int* kernel_kind) {
   g_error.clear();

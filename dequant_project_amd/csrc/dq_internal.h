@@ -68,6 +68,14 @@ constexpr int64_t kGemmScratchBytes = int64_t(8) << 20;
 hipError_t launch_gemm_batch(const GemvOperand* ops, int count, int64_t M, int bits, bool symmetric,
                              bool interleaved, void* scratch, hipStream_t stream);
 
+// Split along K of a launch_gemm_batch launch with a scratch (pure host
+// logic): gemm_walk_splits gives the launch's split factor S (1: unsplit, as
+// for M <= 16 or without a scratch), gemm_problem_splits the blocks per column
+// group of a problem with K columns under it. A problem with more than one
+// runs as two kernel launches (the walk, then the sum of its partials).
+int gemm_walk_splits(const GemvOperand* ops, int count, int64_t M, int bits, bool scratch);
+int gemm_problem_splits(int64_t K, int bits, int S);
+
 // Device address, on the current device, of the library's static scratch
 // (kGemmScratchBytes) for dq_gemm_small_noalloc; allocates nothing.
 hipError_t gemm_static_scratch(void** out);

@@ -2790,20 +2790,10 @@ constexpr int kWalkBlocks = 160;
 template <int BITS, bool SYM, bool INTER, int MB>
 hipError_t launch_gemm_walk(const GemvOperand* ops, int count, int64_t M, void* scratch, hipStream_t stream) {
   constexpr int CPL = 128 / BITS;
-  constexpr int64_t TILE = 16 * MB * kTileCols;
   GemmBatch gb{};
   gb.count = count;
   gb.M = static_cast<int>(M);
-  int64_t groups = 0;
-  for (int i = 0; i < count; ++i) groups += (ops[i].N + kTileCols - 1) / kTileCols;
-  int S = 1;
-  if (scratch != nullptr) {
-    int64_t min_iters = INT64_MAX;
-    for (int i = 0; i < count; ++i) min_iters = std::min<int64_t>(min_iters, (ops[i].K / CPL + 3) / 4);
-    while (groups * S < kWalkBlocks && min_iters / (2 * S) >= kWalkDepth &&
-           groups * 2 * S * TILE * 4 <= kGemmScratchBytes)
-      S *= 2;
-  }
+  const int S = gemm_walk_splits(ops, count, M, BITS, scratch != nullptr);
   GemmBatch sum{};  // the second launch: one block per split column group
   sum.count = count;
   sum.M = gb.M;
@@ -2826,7 +2816,7 @@ hipError_t launch_gemm_walk(const GemvOperand* ops, int count, int64_t M, void* 
     const int iters = (k.n_chunks + 3) / 4;
     const int g = static_cast<int>((o.N + kTileCols - 1) / kTileCols);
     k.ips = ((iters + S - 1) / S + kWalkDepth - 1) / kWalkDepth * kWalkDepth;
-    k.splits = (iters + k.ips - 1) / k.ips;
+    k.splits = gemm_problem_splits(o.K, BITS, S);
     k.part_base = tiles;
     gb.bt_start[i] = bts;
     bts += g * k.splits;
@@ -2989,6 +2979,27 @@ hipError_t launch_gemv_prologue_batch(const GemvOperand* ops, int count, int64_t
 #define DQ_CALL_PRO(B, S, I) launch_gemv_prologue_t<B, S, I>(ops, count, M, prologue, eps, stream)
   DQ_DISPATCH_12(bits, symmetric, interleaved, DQ_CALL_PRO)
 #undef DQ_CALL_PRO
+}
+
+int gemm_walk_splits(const GemvOperand* ops, int count, int64_t M, int bits, bool scratch) {
+  if (M <= 16 || !scratch) return 1;
+  const int64_t cpl = 128 / bits;
+  const int64_t tile = 16 * (M > 32 ? 4 : 2) * kTileCols;
+  int64_t groups = 0, min_iters = INT64_MAX;
+  for (int i = 0; i < count; ++i) {
+    groups += (ops[i].N + kTileCols - 1) / kTileCols;
+    min_iters = std::min<int64_t>(min_iters, (ops[i].K / cpl + 3) / 4);
+  }
+  int S = 1;
+  while (groups * S < kWalkBlocks && min_iters / (2 * S) >= kWalkDepth && groups * 2 * S * tile * 4 <= kGemmScratchBytes)
+    S *= 2;
+  return S;
+}
+
+int gemm_problem_splits(int64_t K, int bits, int S) {
+  const int iters = static_cast<int>((K / (128 / bits) + 3) / 4);
+  const int ips = ((iters + S - 1) / S + kWalkDepth - 1) / kWalkDepth * kWalkDepth;
+  return (iters + ips - 1) / ips;
 }
 
 // Scratch of dq_gemm_small_noalloc, for callers that cannot allocate: the

@@ -216,6 +216,15 @@ int dq_gemm_small(const dq_gemv_problem* problems, int count, int64_t M, int64_t
 int dq_gemm_small_noalloc(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int symmetric,
                           int interleaved, dq_stream_t stream);
 
+/* Split along K that dq_gemm_small / dq_gemm_small_noalloc would use for
+ * these problems (no reference counterpart; pure host logic), for profiling
+ * and tuning tools: splits[i] = blocks per 64-column group of problem i along
+ * K (1: unsplit, always for M <= 16). A launch with any problem above 1 runs
+ * as two kernels (gemm_walk_kernel, then gemm_split_sum_kernel summing its
+ * partial tiles). Weights past 2 GiB, which dq_gemm_small launches as row
+ * slices, are planned here as one problem. */
+int dq_gemm_small_plan(const dq_gemv_problem* problems, int count, int64_t M, int64_t bits, int* splits);
+
 /* Geometry the launch of these problems would use (no reference
  * counterpart), for profiling and tuning tools; pure host logic. For each
  * problem i, waves_per_tile[i] waves (1, 2 or 4) share one tile along K;

@@ -195,6 +195,38 @@ def test_torch_binding_rejects_cpu_tensors_with_reference_messages():
         ext.unpack(qweight=qw, bits=4, interleaved=False, K=256)
 
 
+def test_gemm_small_plan_splits():
+    """dq_gemm_small_plan (host logic): launches with 16 < M split K across
+    blocks while the column groups (64 columns each) give fewer than 160
+    blocks, at least one 4-iteration trip per split; M <= 16 never splits."""
+    lib = _native.capi()
+
+    def plan(m, shapes, bits=4):
+        arr = (_native.DqGemvProblem * len(shapes))()
+        for i, (n, k) in enumerate(shapes):
+            arr[i].N, arr[i].K, arr[i].group_size = n, k, 128
+        sp = (ctypes.c_int * len(shapes))()
+        assert lib.dq_gemm_small_plan(arr, len(shapes), m, bits, sp) == 0, lib.dq_last_error()
+        return list(sp)
+
+    q, kv, gate, down = (4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)
+    for m in (9, 16):
+        assert plan(m, [q, kv, gate, down]) == [1, 1, 1, 1]
+    for m in (17, 64):
+        # 64 groups: 4 splits (256 blocks); 16 groups: 8 (32 iterations, 4 each); 224 groups: none
+        assert plan(m, [q]) == [4] and plan(m, [kv]) == [8] and plan(m, [gate]) == [1] and plan(m, [down]) == [4]
+    assert plan(64, [q, kv]) == [2, 2]       # 80 groups together: 2 splits
+    assert plan(64, [(1000, 96)]) == [1]     # one iteration: nothing to split
+    assert plan(64, [q], bits=8) == [4] and plan(64, [q], bits=2) == [4]
+    arr = (_native.DqGemvProblem * 1)()
+    arr[0].N, arr[0].K, arr[0].group_size = 64, 256, 128
+    sp = (ctypes.c_int * 1)()
+    assert lib.dq_gemm_small_plan(arr, 1, 65, 4, sp) == 2
+    assert lib.dq_last_error().startswith(b"gemm_small handles 1 <= M <= 64, got M=65")
+    assert lib.dq_gemm_small_plan(arr, 1, 64, 3, sp) == 1
+    assert lib.dq_gemm_small_plan(arr, 1, 64, 4, None) == 1
+
+
 def test_gemv_plan_geometry():
     """dq_gemv_plan (host logic): launch geometry chosen per launch from the problems' shapes."""
     lib = _native.capi()
