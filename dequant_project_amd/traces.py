@@ -133,6 +133,9 @@ def render(records, line, stats, command, unprofiled=None):
            "rocprofv3 kernel trace of bench.py with the driver's flags; per timed leg and kernel",
            "instance, the durations of the timed graph replays (warm-up replays dropped). GB/s =",
            "the launches' algorithmic bytes (from the counter pass) / their summed durations.",
+           "Leg step us = the leg's timed span / steps under the profiler, which adds per-dispatch",
+           "overhead to the legs of many short launches (decode, per-linear): their unprofiled",
+           "per-layer times are in the bench line (modes, read_floors), not in that column.",
            "Commands (MI355X, ROCm 7.2):", "", "```"] + command + ["```", ""]
     if kern:
         x5 = [r for r in records if r["leg"] == "C4 stack x5" and r["kernel"].startswith(kern[:-1])]
