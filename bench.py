@@ -186,6 +186,8 @@ class Engine:
         fmt = f"{cfg.bits}, {str(cfg.symmetric).lower()}, {str(cfg.layout == 'interleaved').lower()}"
         if kind.value == 1:
             return f"gemv_quad_kernel<{fmt}, {rows.value // 4}, {1 if m <= 4 else 2}>", tuple(wk)
+        if kind.value == 7:
+            return f"gemv_mx_pipe_kernel<{fmt}, {rows.value}, 2>", tuple(wk)
         if kind.value == 4:
             return f"gemv_m1_pipe_kernel<{fmt}, {rows.value}>", tuple(wk)
         if kind.value in (5, 6):

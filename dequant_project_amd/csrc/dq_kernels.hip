@@ -505,14 +505,23 @@ __device__ __forceinline__ void finish_tile(const KernelProblem& d, const TilePo
 // with S and C taken once per lane and batch (the activations are shared by
 // the tile's R rows). Every product is exact (fp16 operands, fp32 products)
 // and the sums run in fp32; the bias terms cancel in the subtraction, so the
-// sums' rounding error grows with the bias. The codes are therefore placed as
-// high in the mantissa as one shift per copy of the word allows:
+// sums' rounding error grows with the bias. The codes are therefore placed
+// high in the mantissa:
 //   INT4  every nibble at bit 4 (bias 64), from w << 4, w, w >> 4, w >> 8;
-//   INT2  codes at bits 4 / 6 / 8 (bias 64 / 16 / 4), from w << 4, w, w >> 6;
+//   INT2  codes at bits 8 / 6 (bias 4 / 16), from w << 8, w << 4, w, w >> 4,
+//         w >> 6;
 //   INT8  the byte at bit 0 (bias 1024), by byte permutation.
 // A CPU model of this summation order puts its error at under a quarter of
 // the fp32 budget of the reference's kernel test (2^-20 sum |w||x|, its
-// scripts/test_dequant_kernel.py:112-122; exact (q - z) products: ~1%). The
+// scripts/test_dequant_kernel.py:112-122; exact (q - z) products: ~1%) on
+// the Llama shapes, and with that test's fp16 output term, under a third of
+// its tolerance down to K = 128 (INT2: under a half). INT2's 2-bit codes
+// gain least from a bias: with |q - z| <= 2 the earlier placement at bits
+// 4 / 6 / 8 (bias 64 / 16 / 4, two shifts fewer per word) exceeded that
+// tolerance up to 4.4x at K = 128 and 3.3x at K = 256 (rows whose codes sit
+// mostly at the zero point), and a GPU test hit 2.4x at K = 128; every code
+// at bit 8 (bias 4, 0.3x) took three shifts more per word than the current
+// placement and cost the INT2 stacks 10%. The
 // form holds for any zero point (the packer's zeros are unclamped,
 // packer.py:136-137), so there is no separate path for large zero points.
 //   * MF = false: products and sums with v_dot2_f32_f16 (VALU);
@@ -530,16 +539,9 @@ __device__ __forceinline__ h4 cat2(h2 a, h2 b) { return __builtin_shufflevector(
 // Pair i of a word holds slots i and i + PER/2 (the pair order of
 // x_pairs_from_dwords); its codes sit at mantissa bit pow(cls(i)).
 template <int BITS> struct Biased {
-  static constexpr int NCLS = BITS == 2 ? 3 : 1;
-  static constexpr __device__ int cls(int i) {
-    if constexpr (BITS == 2) {
-      constexpr int t[8] = {0, 1, 0, 1, 2, 0, 1, 2};
-      return t[i];
-    } else {
-      return 0;
-    }
-  }
-  static constexpr int pow(int c) { return BITS == 8 ? 0 : 4 + 2 * c; }
+  static constexpr int NCLS = BITS == 2 ? 2 : 1;
+  static constexpr __device__ int cls(int i) { return BITS == 2 && (i == 1 || i == 3 || i == 5) ? 1 : 0; }
+  static constexpr int pow(int c) { return BITS == 8 ? 0 : (BITS == 4 ? 4 : (c == 0 ? 8 : 6)); }
   static constexpr float bias(int c) { return static_cast<float>(1 << (10 - pow(c))); }
   static constexpr uint32_t magic(int c) {
     const uint32_t e = static_cast<uint32_t>(25 - pow(c));
@@ -582,16 +584,18 @@ __device__ __forceinline__ void biased_pairs(uint32_t w, const ClassMagics<BITS>
     p[2] = ((w >> 4) & kNib) | cm.m[0];
     p[3] = ((w >> 8) & kNib) | cm.m[0];
   } else {
-    constexpr uint32_t k4 = 0x00300030u, k6 = 0x00C000C0u, k8 = 0x03000300u;
-    const uint32_t wl = w << 4, wr = w >> 6;
-    p[0] = (wl & k4) | cm.m[0];  // slot 0: bit 0 -> 4
-    p[1] = (wl & k6) | cm.m[1];  // slot 1: bit 2 -> 6
-    p[2] = (w & k4) | cm.m[0];   // slot 2: bit 4
+    // slot i sits at bit 2i of the low half and slot i + 8 at the same offset
+    // of the high half: one shift moves both, to bit 8 (class 0) or 6 (class 1)
+    constexpr uint32_t k8 = 0x03000300u, k6 = 0x00C000C0u;
+    const uint32_t w8 = w << 8, w4 = w << 4, r4 = w >> 4, r6 = w >> 6;
+    p[0] = (w8 & k8) | cm.m[0];  // slot 0: bit 0 -> 8
+    p[1] = (w4 & k6) | cm.m[1];  // slot 1: bit 2 -> 6
+    p[2] = (w4 & k8) | cm.m[0];  // slot 2: bit 4 -> 8
     p[3] = (w & k6) | cm.m[1];   // slot 3: bit 6
-    p[4] = (w & k8) | cm.m[2];   // slot 4: bit 8
-    p[5] = (wr & k4) | cm.m[0];  // slot 5: bit 10 -> 4
-    p[6] = (wr & k6) | cm.m[1];  // slot 6: bit 12 -> 6
-    p[7] = (wr & k8) | cm.m[2];  // slot 7: bit 14 -> 8
+    p[4] = (w & k8) | cm.m[0];   // slot 4: bit 8
+    p[5] = (r4 & k6) | cm.m[1];  // slot 5: bit 10 -> 6
+    p[6] = (r4 & k8) | cm.m[0];  // slot 6: bit 12 -> 8
+    p[7] = (r6 & k8) | cm.m[0];  // slot 7: bit 14 -> 8
   }
 }
 
@@ -1191,6 +1195,128 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     if constexpr (RMS) pair_stage_rmsnorm<BITS>(raw, gam, ssq);
     pair_stage_write<BITS, INTER>(xs + par * PS::kBufBytes, raw);
     lds_barrier();  // the other buffer was read before the previous barrier
+    cb = ncb;
+    bt = nbt;
+    p = np;
+    t = nt;
+  }
+}
+
+// Batches of 2 <= M <= MX rows (the launcher uses MX = 2) on gemv_m1_pipe_kernel's walk:
+// each weight row's biased pairs are formed once per chunk and dotted with
+// every batch row's activations (v_dot2, one fp32 chain per row and batch
+// row, the M = 1 kernel's arithmetic), the activations of all MX batch rows
+// staged per block as there (MX buffers per batch, double-buffered) and the
+// bias sums S, C taken per batch row. One-wave tiles only: launches that
+// split K run gemv_quad_kernel. Batch rows past M load zeros and store
+// nothing.
+template <int BITS, bool SYM, bool INTER, int R, int MX>
+__global__ void __launch_bounds__(kGemvThreads) gemv_mx_pipe_kernel(const KernelBatch b) {
+  using F = Fmt<BITS>;
+  using PS = PairStage<BITS>;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  __shared__ __align__(16) unsigned char xs[2 * MX * PS::kBufBytes];
+  ClassMagics<BITS> cm;
+  cm.init();
+  const int total = b.bt_start[b.count];
+  int p = 0;
+  int bt = static_cast<int>(blockIdx.x);
+  if (bt >= total) return;  // block-uniform: the whole block leaves
+  TilePos t = locate(b, bt, wave, R, p);
+  int cb = t.cb;
+  int par = 0;
+  BatchAddr<R> a;
+  uint32_t raw[MX][PS::kWordDwords];
+  uint32_t z[R], s[R];
+  u32x4 w[R];
+  auto stage_issue = [&](const KernelProblem& d, int cbase, int ce, bool live) {
+#pragma unroll
+    for (int m = 0; m < MX; ++m)
+      pair_stage_issue<BITS>(d.x + static_cast<int64_t>(m) * d.K, d, cbase, ce, live && m < b.M, raw[m]);
+  };
+  auto stage_write = [&](int parity) {
+#pragma unroll
+    for (int m = 0; m < MX; ++m) pair_stage_write<BITS, INTER>(xs + (parity * MX + m) * PS::kBufBytes, raw[m]);
+  };
+  // the first batch: activations staged, rows in flight
+  stage_issue(b.p[t.p], cb, t.ce, true);
+  batch_addr<BITS, SYM, R>(b.p[t.p], t.row0, cb, t.ce, lane, t.active, a);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    issue_row<SYM, R>(a, r, z[r], s[r], w[r]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  stage_write(0);
+  lds_barrier();
+  float yacc[MX][R];
+#pragma unroll
+  for (int m = 0; m < MX; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) yacc[m][r] = 0.f;
+  for (;;) {
+    // where the next batch is: the next 64 columns of this tile, or the
+    // first batch of the next block-tile (the same for the whole block)
+    int ncb = cb + 64;
+    int nbt = bt, np = p;
+    TilePos nt = t;
+    const bool tile_end = ncb >= t.ce;
+    if (tile_end) {
+      nbt = bt + static_cast<int>(gridDim.x);
+      if (nbt < total) {
+        nt = locate(b, nbt, wave, R, np);
+        ncb = nt.cb;
+      }
+    }
+    const bool nvalid = nbt < total;  // block-uniform
+    // the current batch's pairs and bias sums, per batch row
+    h2 xr[MX][4][F::PAIRS];
+    float S[MX], C[MX];
+#pragma unroll
+    for (int m = 0; m < MX; ++m) {
+      pair_stage_read<BITS>(xs + (par * MX + m) * PS::kBufBytes, lane, xr[m]);
+      bias_sums<BITS>(xr[m], S[m], C[m]);
+      if constexpr (SYM) C[m] = __builtin_fmaf(static_cast<float>(F::BIAS), S[m], C[m]);
+    }
+    // the next batch's activations, then its rows as the current ones free their registers
+    stage_issue(b.p[np], ncb, nt.ce, nvalid);
+    batch_addr<BITS, SYM, R>(b.p[np], nt.row0, ncb, nt.ce, lane, nvalid && nt.active, a);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint32_t mp[4][F::PAIRS];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) biased_pairs<BITS>(w[r][j], cm, mp[j]);
+      const float zf = SYM ? 0.f : f16_to_f32(static_cast<uint16_t>(z[r]));
+      const float sf = f16_to_f32(static_cast<uint16_t>(s[r]));
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+        float v = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < F::PAIRS; ++i) v = __builtin_amdgcn_fdot2(as_h2(mp[j][i]), xr[m][j][i], v, false);
+        const float corr = SYM ? C[m] : __builtin_fmaf(zf, S[m], C[m]);
+        yacc[m][r] = __builtin_fmaf(sf, v - corr, yacc[m][r]);
+      }
+      issue_row<SYM, R>(a, r, z[r], s[r], w[r]);  // row r of the next batch, into the freed registers
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (tile_end) {
+      const KernelProblem& d = b.p[t.p];
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+        wave_sum_rows<R>(yacc[m]);
+        if (m < b.M && t.active && (lane & 15) == 15)
+          store_rows<R / 4>(d.y + static_cast<int64_t>(m) * d.ldy, t.row0 + (lane >> 4) * (R / 4), d.N, yacc[m]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) yacc[m][r] = 0.f;
+      }
+    }
+    if (!nvalid) break;
+    par ^= 1;
+    stage_write(par);
+    lds_barrier();  // the other buffers were read before the previous barrier
     cb = ncb;
     bt = nbt;
     p = np;
@@ -2845,11 +2971,41 @@ hipError_t launch_gemm_t(const GemvOperand* ops, int count, int64_t M, void* scr
   return launch_gemm_mb<BITS, SYM, INTER, 4>(ops, count, M, stream);
 }
 
+// Batches of 2 rows run gemv_mx_pipe_kernel<..., MX = 2> when the M = 1 rule
+// gives every problem one-wave tiles; the others run gemv_quad_kernel.
+// Measured on the C4 stack: M = 2 25.29 -> 22.82 us/layer; at M = 4 the
+// four-row instance (192 VGPRs, two waves per SIMD) ran 33.3 us/layer
+// against the quad kernel's 26.8, so M >= 3 stays there.
+constexpr bool mx_pipe_fits(int, int64_t M) { return M == 2; }
+
+bool mx_pipe_plan(const GemvOperand* ops, int count, int64_t M, int bits, int* R, int* wks) {
+  if (!mx_pipe_fits(bits, M)) return false;
+  *R = rows_per_tile(ops, count);
+  waves_per_tile(ops, count, bits, *R, wks);
+  for (int i = 0; i < count; ++i)
+    if (wks[i] != 1) return false;
+  return true;
+}
+
+template <int BITS, bool SYM, bool INTER, int R, int MX>
+hipError_t launch_gemv_mx(const GemvOperand* ops, int count, int64_t M, const int* wks, hipStream_t stream) {
+  KernelBatch kb;
+  const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
+  if (bts == 0) return hipSuccess;
+  constexpr auto kernel = gemv_mx_pipe_kernel<BITS, SYM, INTER, R, MX>;
+  return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+}
+
 template <int BITS, bool SYM, bool INTER>
 hipError_t launch_gemv_t(const GemvOperand* ops, int count, int64_t M, hipStream_t stream) {
   if (M == 1) {
     if (rows_per_tile(ops, count) == 8) return launch_gemv_m1<BITS, SYM, INTER, 8>(ops, count, M, stream);
     return launch_gemv_m1<BITS, SYM, INTER, 4>(ops, count, M, stream);
+  }
+  int R = 0, wks[kMaxBatch];
+  if (mx_pipe_plan(ops, count, M, BITS, &R, wks)) {
+    return R == 8 ? launch_gemv_mx<BITS, SYM, INTER, 8, 2>(ops, count, M, wks, stream)
+                  : launch_gemv_mx<BITS, SYM, INTER, 4, 2>(ops, count, M, wks, stream);
   }
   if (M <= 4) return launch_gemv_quad<BITS, SYM, INTER, 1>(ops, count, M, stream);
   return launch_gemv_quad<BITS, SYM, INTER, 2>(ops, count, M, stream);
@@ -2935,6 +3091,10 @@ hipError_t launch_unpack_t(const uint32_t* qweight, int32_t* out, int64_t N, int
   }
 
 void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows, int* mfma) {
+  if (mx_pipe_plan(ops, count, M, bits, rows, wk)) {
+    *mfma = 7;
+    return;
+  }
   if (M >= 2) {
     *mfma = 1;
     *rows = 4 * kQuadsPerTile;

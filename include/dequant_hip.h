@@ -231,7 +231,8 @@ int dq_gemm_small_plan(const dq_gemv_problem* problems, int count, int64_t M, in
  * the launch uses *rows_per_tile output rows per tile and the kernel
  *   *kernel_kind == 1: gemv_quad_kernel<bits, symmetric, interleaved,
  *                      rows_per_tile / 4, MG> (matrix cores; 2 <= M <= 8,
- *                      any group size; MG = 1 for M <= 4, else 2),
+ *                      any group size; MG = 1 for M <= 4, else 2; for
+ *                      M = 2 only launches that kind 7 does not take),
  *   *kernel_kind == 2: gemv_m1_kernel<bits, symmetric, interleaved,
  *                      rows_per_tile, false> (M = 1; VALU dot products), or
  *   *kernel_kind == 3: gemv_m1_kernel<bits, symmetric, interleaved,
@@ -246,7 +247,11 @@ int dq_gemm_small_plan(const dq_gemv_problem* problems, int count, int64_t M, in
  *                      enough rounds of its persistent grid),
  *   *kernel_kind == 6: gemv_m1_kernel's INT2 variant that keeps a wave's
  *                      activations across consecutive 8-row one-batch tiles
- *                      (K <= 4096, at least two rounds of its grid).
+ *                      (K <= 4096, at least two rounds of its grid),
+ *   *kernel_kind == 7: gemv_mx_pipe_kernel<bits, symmetric, interleaved,
+ *                      rows_per_tile, 2> (M = 2, launches whose tiles are
+ *                      all one wave wide: kind 4's walk with each weight
+ *                      chunk dotted with both batch rows).
  * Kinds 5 and 6 depend on the device's co-resident blocks; without a device
  * the plan assumes 256 CUs.
  * The geometry is chosen per launch, so a problem's result is deterministic

@@ -259,14 +259,21 @@ def test_gemv_plan_geometry():
     assert plan([(14336, 4096)] * 2, bits=2, gs=64) == ([1, 1], 4, 4)     # INT2 decode gate | up: pipelined
     assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 2)  # 172 columns of 64 codes, 43 per wave
     assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 2)  # INT8 wants 8192 waves
-    # 2 <= M <= 8: gemv_quad_kernel (kind 1) for every format and group size;
-    # 8-row tiles (two quads), wk by the M = 1 rule for 8-row tiles.
+    # M = 2, launches whose M = 1 plan has one-wave tiles: gemv_mx_pipe_kernel
+    # (kind 7) with the M = 1 rows per tile.
+    assert plan([(14336, 4096)] * 16, m=2) == ([1] * 16, 8, 7)
+    assert plan([(14336, 4096)] * 2, m=2) == ([1, 1], 4, 7)
+    assert plan([(14336, 4096)] * 16, m=2, bits=2, gs=64) == ([1] * 16, 8, 7)
+    # the others, and 3 <= M <= 8: gemv_quad_kernel (kind 1) for every format and
+    # group size; 8-row tiles (two quads), wk by the M = 1 rule for 8-row tiles.
+    assert plan([(14336, 4096)] * 16, m=4) == ([1] * 16, 8, 1)
+    assert plan([(14336, 4096)] * 2, m=3) == ([2, 2], 8, 1)
     assert plan([(4096, 4096)], m=4) == ([2], 8, 1)
     assert plan([(14336, 4096)] * 2, m=8) == ([2, 2], 8, 1)
     assert plan([(11008, 4096)], m=4, bits=8, gs=None) == ([2], 8, 1)  # INT8 quad launches: 2048 waves
     assert plan([(4096, 11008)], m=4, bits=2, gs=64) == ([4], 8, 1)
     assert plan([(4096, 4096)], m=2, gs=64) == ([2], 8, 1)
-    assert plan([(14336, 4096)] * 16, m=2) == ([1] * 16, 8, 1)
+    assert plan([(14336, 4096)] * 16, m=8) == ([1] * 16, 8, 1)
     arr = (_native.DqGemvProblem * 1)()
     arr[0].N, arr[0].K, arr[0].group_size = 8, 100, 100
     wk, rows, kind = (ctypes.c_int * 1)(), ctypes.c_int(), ctypes.c_int()

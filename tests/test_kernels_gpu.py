@@ -603,7 +603,7 @@ def test_grouped_launch_matches_oracle_and_single_calls(torch_gpu, m):
     GROUPED_VS_SINGLE_REL_L2: a grouped launch may split a tile's K over a
     different number of waves than the single call, which changes the fp32
     summation order; the M = 1 kernel sums (bias + q) x products, with a
-    bias of 64 (INT4), 64 / 16 / 4 (INT2) or 1024 (INT8) that cancels only
+    bias of 64 (INT4), 4 (INT2) or 1024 (INT8) that cancels only
     at the end, so about 0.3% of the fp16 outputs round to the neighbouring
     value (rel-L2 ~2e-5). 1e-4 still sits 10x below the oracle's 1e-3."""
     torch = torch_gpu
@@ -756,6 +756,51 @@ def test_pipelined_m1_kernel_walk(torch_gpu, bits, gs, sym, layout, shapes, rows
         single = ext().gemv(x, *ext_args(pw)).float()
         diff = (ys[i].float() - single).norm() / single.norm().clamp_min(1e-30)
         assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
+
+
+@pytest.mark.parametrize("bits,gs,sym,layout,shapes,rows_per_tile,m", [
+    # the pipelined M = 1 walk's launches (one-wave tiles) at 2 batch rows:
+    # ragged rows, partial last batches, a one-row problem (INT4 g32, 8-row tiles)
+    (4, 32, True, "interleaved", [(5003, 5120), (7001, 3072), (9999, 5120), (30005, 1056), (1, 5120),
+                                  (20000, 4096)], 8, 2),
+    (4, 128, False, "sequential", [(14336, 4096), (14336, 4096)], 4, 2),
+    (8, None, True, "interleaved", [(11008, 4096), (11008, 4096), (11008, 4096), (5, 4096)], 4, 2),
+    (8, 64, False, "sequential", [(4100, 14336)] * 16, 8, 2),
+    (2, 64, False, "sequential", [(14336, 4096), (14336, 4096)], 4, 2),
+    # INT2 symmetric with a K = 128 problem (two chunks per row: rows whose
+    # codes sit mostly at the zero point have the smallest tolerance)
+    (2, 128, True, "interleaved", [(9001, 7680), (5003, 4096), (777, 128), (2, 7680), (3000, 4096)], 4, 2),
+])
+def test_pipelined_batch_rows_walk(torch_gpu, bits, gs, sym, layout, shapes, rows_per_tile, m):
+    """gemv_mx_pipe_kernel (kind 7 of dq_gemv_plan): the pipelined walk with
+    two batch rows, each weight chunk dotted with both. Every problem against
+    the oracle on a sample of rows that includes its last 40, both batch
+    rows, and deterministic."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    wk, r, kind = _plan(shapes, bits, gs, m)
+    assert (wk, r, kind) == ([1] * len(shapes), rows_per_tile, 7)
+    gen = torch.Generator(device="cuda").manual_seed(bits * 11 + len(shapes) + m)
+    cfg = QuantConfig(bits, gs, sym, layout)
+    pws, cases, xs, x16s = [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        pw = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02, cfg)
+        rng = np.random.Generator(np.random.PCG64(700 + i))
+        rows = np.unique(np.concatenate([rng.choice(n, min(n, 160), replace=False), np.arange(max(0, n - 40), n)]))
+        qw, sc = pw.qweight.cpu().numpy(), pw.scales.cpu().numpy()
+        ze = None if pw.zeros is None else pw.zeros.cpu().numpy()
+        cases.append(OracleCase(pw, qw, sc, ze, rows, deq_ref=False))
+        x16s.append(activations(m, k, seed=800 + i))
+        xs.append(to_gpu(torch, x16s[-1]))
+        pws.append(pw)
+    args = ([p.qweight for p in pws], [p.scales for p in pws], [p.zeros for p in pws], bits,
+            [p.config.effective_group_size(p.shape[1]) for p in pws], sym, layout == "interleaved")
+    ys = ext().gemv_batched(xs, *args)
+    again = ext().gemv_batched(xs, *args)
+    for i in range(len(pws)):
+        assert torch.equal(ys[i], again[i]), f"problem {i}: not deterministic"
+        cases[i].check(ys[i].cpu().numpy(), x16s[i], f"pipelined M={m} INT{bits} {shapes[i]} problem {i}")
 
 
 def test_int2_shared_and_mixed_activations_across_tiles(torch_gpu):
