@@ -2549,6 +2549,27 @@ void waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk,
   }
 }
 
+// wk for an M = 1 launch whose kernel can be gemv_m1_pipe_kernel (no
+// prologue, or RMSNorm): one-wave tiles, in place of the K split above, for
+// every INT2 launch and for INT4 / INT8 launches of at most kPipeTiles tiles.
+// The pipelined kernel (or an INT2 staged / kept variant) then walks whole
+// rows with the activations staged per block. Measured against the K split
+// (graph replays of distinct weights): INT2 8192 x 28672 (C5 down_proj)
+// 24.1 -> 16.9 us, 4096 x 14336 8.57 -> 7.52, 4096 x 11008 (C3) 7.39 ->
+// 6.42; INT4 4096 x 4096 (C1, C4 o_proj; 1024 tiles) 4.72 -> 4.20,
+// 4096 x 14336 (C4 down_proj) 9.15 -> 8.75; but INT4 C4 q|k|v (1536 tiles)
+// 5.10 -> 5.22, C5 o_proj (2048) 9.33 -> 9.7, C5 q|k|v (2560) 10.8 -> 11.8,
+// INT8 11008 x 4096 (C2, 2752 tiles) 9.24 -> 10.32.
+constexpr int64_t kPipeTiles = 1024;
+
+void m1_waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk) {
+  waves_per_tile(ops, count, bits, R, wk);
+  int64_t tiles = 0;
+  for (int i = 0; i < count; ++i) tiles += (ops[i].N + R - 1) / R;
+  if (bits == 2 || tiles <= kPipeTiles)
+    for (int i = 0; i < count; ++i) wk[i] = 1;
+}
+
 int log2_exact(int64_t v) {  // log2 of a power of two, else -1
   if (v <= 0 || (v & (v - 1)) != 0) return -1;
   int s = 0;
@@ -2709,7 +2730,8 @@ M1Variant m1_variant(const KernelBatch& kb, int count, int bits, int R, const in
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
   int wks[kMaxBatch];
-  waves_per_tile(ops, count, BITS, R, wks);
+  if constexpr (PRO == kProNone || PRO == kProRmsNorm) m1_waves_per_tile(ops, count, BITS, R, wks);
+  else waves_per_tile(ops, count, BITS, R, wks);
   KernelBatch kb;
   const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
   kb.eps = eps;
@@ -3104,7 +3126,8 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
   }
   *mfma = M == 1 ? (m1_uses_mfma(bits) ? 3 : 2) : 0;
   *rows = rows_per_tile(ops, count);
-  waves_per_tile(ops, count, bits, *rows, wk);
+  if (M == 1) m1_waves_per_tile(ops, count, bits, *rows, wk);
+  else waves_per_tile(ops, count, bits, *rows, wk);
   if (M == 1 && !m1_uses_mfma(bits)) {
     // the INT2 staged / kept variants hold four blocks per CU; the launch
     // itself asks the device for its kernel's co-resident blocks

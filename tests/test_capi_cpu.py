@@ -244,20 +244,24 @@ def test_gemv_plan_geometry():
     # or gemv_m1_pipe_kernel (kind 4) when every problem's tiles are one wave wide
     # (INT4 and INT8). INT4: 32 codes per 16-byte column. Rows per tile: 8 for
     # launches with >= 6144 tiles of 8 rows, else 4. wk: smallest of 1, 2, 4 giving
-    # the launch 6144 waves (INT4), capped so each wave keeps >= 40 columns.
+    # the launch 6144 waves (INT4), capped so each wave keeps >= 40 columns; but
+    # one-wave tiles for INT2 launches and for launches of at most 1024 tiles.
     assert plan([(14336, 4096)]) == ([2], 4, 2)
     assert plan([(14336, 4096)] * 2) == ([1, 1], 4, 4)          # gate | up: 7168 waves already
-    assert plan([(4096, 14336)]) == ([4], 4, 2)                 # 448 columns: 112 per wave
-    assert plan([(4096, 4096)]) == ([2], 4, 2)                  # 128 columns: 4 waves would leave 32
-    assert plan([(1024, 4096)]) == ([2], 4, 2)
-    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 2)
+    assert plan([(4096, 14336)]) == ([1], 4, 4)                 # 1024 tiles: one wave each
+    assert plan([(4096, 4096)]) == ([1], 4, 4)
+    assert plan([(1024, 4096)]) == ([1], 4, 4)
+    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 2)  # 1536 tiles: split
+    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)], bits=8, gs=128) == ([4, 4, 4], 4, 2)
+    assert plan([(8192, 8192)]) == ([4], 4, 2)                  # 2048 tiles: 64 columns per wave
     assert plan([(14336, 4096)] * 16) == ([1] * 16, 8, 4)       # a stack of projections: 8-row tiles
     assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 4)
     assert plan([(4096, 14336)] * 16, bits=8, gs=None) == ([1] * 16, 8, 4)
     assert plan([(14336, 4096)] * 16, bits=2, gs=64) == ([1] * 16, 8, 6)  # INT2: activations kept across tiles
     assert plan([(14336, 8192)] * 16, bits=2, gs=64) == ([1] * 16, 8, 5)  # INT2: activations staged per block
     assert plan([(14336, 4096)] * 2, bits=2, gs=64) == ([1, 1], 4, 4)     # INT2 decode gate | up: pipelined
-    assert plan([(4096, 11008)], bits=2, gs=64) == ([4], 4, 2)  # 172 columns of 64 codes, 43 per wave
+    assert plan([(4096, 11008)], bits=2, gs=64) == ([1], 4, 4)  # INT2: one-wave tiles, pipelined
+    assert plan([(8192, 28672)], bits=2, gs=64) == ([1], 4, 4)
     assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 2)  # INT8 wants 8192 waves
     # M = 2, launches whose M = 1 plan has one-wave tiles: gemv_mx_pipe_kernel
     # (kind 7) with the M = 1 rows per tile.
