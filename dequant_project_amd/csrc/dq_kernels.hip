@@ -1055,6 +1055,15 @@ __device__ __forceinline__ void pair_stage_rmsnorm(uint32_t (&raw)[PairStage<BIT
   }
 }
 
+// The SwiGLU prologue on a staged word: x is the gate projection's output,
+// the operand the up projection's (the arithmetic of x_pairs_pro).
+template <int BITS>
+__device__ __forceinline__ void pair_stage_swiglu(uint32_t (&raw)[PairStage<BITS>::kWordDwords],
+                                                  const uint32_t (&up)[PairStage<BITS>::kWordDwords]) {
+#pragma unroll
+  for (int i = 0; i < PairStage<BITS>::kWordDwords; ++i) raw[i] = swiglu_pair(raw[i], up[i]);
+}
+
 template <int BITS, bool INTER>
 __device__ __forceinline__ void pair_stage_write(unsigned char* buf, const uint32_t (&raw)[PairStage<BITS>::kWordDwords]) {
   using PS = PairStage<BITS>;
@@ -1094,13 +1103,16 @@ __device__ __forceinline__ void pair_stage_read(const unsigned char* buf, int la
 // block-tile, by one thread); at the tile's end the block sums those partial
 // sums (every tile of a block-tile shares x) and each row's dot product is
 // multiplied by 1 / sqrt(sum(x^2) / K + eps) before the fp16 store.
+// PRO = kProSwiGlu: the staging threads form silu(gate) * up of the words
+// they stage (x = gate, aux = up), once per block and batch instead of once
+// per tile and lane.
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 __global__ void __launch_bounds__(kGemvThreads)
 gemv_m1_pipe_kernel(const KernelBatch b) {
-  static_assert(PRO == kProNone || PRO == kProRmsNorm, "pipelined prologue");
   using F = Fmt<BITS>;
   using PS = PairStage<BITS>;
   constexpr bool RMS = PRO == kProRmsNorm;
+  constexpr bool SWI = PRO == kProSwiGlu;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   __shared__ __align__(16) unsigned char xs[2 * PS::kBufBytes];
@@ -1116,12 +1128,12 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
   int cb = t.cb;
   int par = 0;
   BatchAddr<R> a;
-  uint32_t raw[PS::kWordDwords], gam[RMS ? PS::kWordDwords : 1];
+  uint32_t raw[PS::kWordDwords], gam[RMS || SWI ? PS::kWordDwords : 1];  // gam: gamma or up
   uint32_t z[R], s[R];
   u32x4 w[R];
   // the first batch: activations staged, rows in flight
   pair_stage_issue<BITS>(b.p[t.p].x, b.p[t.p], cb, t.ce, true, raw);
-  if constexpr (RMS) pair_stage_issue<BITS>(b.p[t.p].aux, b.p[t.p], cb, t.ce, true, gam);
+  if constexpr (RMS || SWI) pair_stage_issue<BITS>(b.p[t.p].aux, b.p[t.p], cb, t.ce, true, gam);
   batch_addr<BITS, SYM, R>(b.p[t.p], t.row0, cb, t.ce, lane, t.active, a);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -1129,6 +1141,7 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     __builtin_amdgcn_sched_barrier(0);
   }
   if constexpr (RMS) pair_stage_rmsnorm<BITS>(raw, gam, ssq);
+  if constexpr (SWI) pair_stage_swiglu<BITS>(raw, gam);
   pair_stage_write<BITS, INTER>(xs, raw);
   lds_barrier();
   float yacc[R];
@@ -1158,7 +1171,7 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     // the next batch's activations (issued first: vmcnt retires in order),
     // then its rows as the current ones free their registers
     pair_stage_issue<BITS>(b.p[np].x, b.p[np], ncb, nt.ce, nvalid, raw);
-    if constexpr (RMS) pair_stage_issue<BITS>(b.p[np].aux, b.p[np], ncb, nt.ce, nvalid, gam);
+    if constexpr (RMS || SWI) pair_stage_issue<BITS>(b.p[np].aux, b.p[np], ncb, nt.ce, nvalid, gam);
     batch_addr<BITS, SYM, R>(b.p[np], nt.row0, ncb, nt.ce, lane, nvalid && nt.active, a);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1193,6 +1206,7 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     if (!nvalid) break;
     par ^= 1;
     if constexpr (RMS) pair_stage_rmsnorm<BITS>(raw, gam, ssq);
+    if constexpr (SWI) pair_stage_swiglu<BITS>(raw, gam);
     pair_stage_write<BITS, INTER>(xs + par * PS::kBufBytes, raw);
     lds_barrier();  // the other buffer was read before the previous barrier
     cb = ncb;
@@ -2549,9 +2563,9 @@ void waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk,
   }
 }
 
-// wk for an M = 1 launch whose kernel can be gemv_m1_pipe_kernel (no
-// prologue, or RMSNorm): one-wave tiles, in place of the K split above, for
-// every INT2 launch and for INT4 / INT8 launches of at most kPipeTiles tiles.
+// wk for an M = 1 launch (gemv_m1_pipe_kernel takes those of one-wave
+// tiles): one-wave tiles, in place of the K split above, for every INT2
+// launch and for INT4 / INT8 launches of at most kPipeTiles four-row tiles.
 // The pipelined kernel (or an INT2 staged / kept variant) then walks whole
 // rows with the activations staged per block. Measured against the K split
 // (graph replays of distinct weights): INT2 8192 x 28672 (C5 down_proj)
@@ -2566,7 +2580,7 @@ void m1_waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* 
   waves_per_tile(ops, count, bits, R, wk);
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i) tiles += (ops[i].N + R - 1) / R;
-  if (bits == 2 || tiles <= kPipeTiles)
+  if (bits == 2 || (R == 4 && tiles <= kPipeTiles))
     for (int i = 0; i < count; ++i) wk[i] = 1;
 }
 
@@ -2730,8 +2744,7 @@ M1Variant m1_variant(const KernelBatch& kb, int count, int bits, int R, const in
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
   int wks[kMaxBatch];
-  if constexpr (PRO == kProNone || PRO == kProRmsNorm) m1_waves_per_tile(ops, count, BITS, R, wks);
-  else waves_per_tile(ops, count, BITS, R, wks);
+  m1_waves_per_tile(ops, count, BITS, R, wks);
   KernelBatch kb;
   const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
   kb.eps = eps;
@@ -2759,11 +2772,11 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
         break;
     }
   }
-  if constexpr (PRO == kProRmsNorm && !m1_uses_mfma(BITS)) {
+  if constexpr ((PRO == kProRmsNorm || PRO == kProSwiGlu) && !m1_uses_mfma(BITS)) {
     bool one_wave = true;
     for (int i = 0; i < count; ++i) one_wave = one_wave && wks[i] == 1;
     if (one_wave) {
-      constexpr auto kernel = gemv_m1_pipe_kernel<BITS, SYM, INTER, R, kProRmsNorm>;
+      constexpr auto kernel = gemv_m1_pipe_kernel<BITS, SYM, INTER, R, PRO>;
       return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
     }
   }
@@ -3061,9 +3074,17 @@ hipError_t launch_gemv_prologue_t(const GemvOperand* ops, int count, int64_t M, 
     return wide_tiles && !one_wave ? launch_gemv_m1<BITS, SYM, INTER, 8, kProRmsNorm>(ops, count, M, stream, eps)
                                    : launch_gemv_m1<BITS, SYM, INTER, 4, kProRmsNorm>(ops, count, M, stream, eps);
   }
-  if (prologue == kPrologueSwiGlu)
-    return wide_tiles ? launch_gemv_m1<BITS, SYM, INTER, 8, kProSwiGlu>(ops, count, M, stream)
-                      : launch_gemv_m1<BITS, SYM, INTER, 4, kProSwiGlu>(ops, count, M, stream);
+  if (prologue == kPrologueSwiGlu) {
+    // SwiGLU launches whose plain-rule tiles are one wave wide (down_proj at
+    // decode) take the pipelined kernel, which forms the prologue once per
+    // block and batch; the others keep 8-row tiles.
+    int wks[kMaxBatch];
+    m1_waves_per_tile(ops, count, BITS, rows_per_tile(ops, count), wks);
+    bool one_wave = rows_per_tile(ops, count) == 4;
+    for (int i = 0; i < count; ++i) one_wave = one_wave && wks[i] == 1;
+    return wide_tiles && !one_wave ? launch_gemv_m1<BITS, SYM, INTER, 8, kProSwiGlu>(ops, count, M, stream)
+                                   : launch_gemv_m1<BITS, SYM, INTER, 4, kProSwiGlu>(ops, count, M, stream);
+  }
   return hipErrorInvalidValue;
 }
 
