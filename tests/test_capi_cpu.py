@@ -253,7 +253,9 @@ def test_gemv_plan_geometry():
     assert plan([(1024, 4096)]) == ([1], 4, 4)
     assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 2)  # 1536 tiles: split
     assert plan([(4096, 4096), (1024, 4096), (1024, 4096)], bits=8, gs=128) == ([4, 4, 4], 4, 2)
-    assert plan([(8192, 8192)]) == ([4], 4, 2)                  # 2048 tiles: 64 columns per wave
+    assert plan([(8192, 8192)]) == ([4], 8, 2)                  # K >= 8192, 1024 tiles of 8 rows: 8-row split
+    assert plan([(8192, 8192), (1024, 8192), (1024, 8192)]) == ([4, 4, 4], 8, 2)
+    assert plan([(4096, 8192)]) == ([1], 4, 4)                  # 512 tiles of 8 rows: the 4-row rule
     assert plan([(14336, 4096)] * 16) == ([1] * 16, 8, 4)       # a stack of projections: 8-row tiles
     assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 4)
     assert plan([(4096, 14336)] * 16, bits=8, gs=None) == ([1] * 16, 8, 4)
@@ -261,7 +263,7 @@ def test_gemv_plan_geometry():
     assert plan([(14336, 8192)] * 16, bits=2, gs=64) == ([1] * 16, 8, 5)  # INT2: activations staged per block
     assert plan([(14336, 4096)] * 2, bits=2, gs=64) == ([1, 1], 4, 4)     # INT2 decode gate | up: pipelined
     assert plan([(4096, 11008)], bits=2, gs=64) == ([1], 4, 4)  # INT2: one-wave tiles, pipelined
-    assert plan([(8192, 28672)], bits=2, gs=64) == ([1], 4, 4)
+    assert plan([(8192, 28672)], bits=2, gs=64) == ([1], 8, 4)
     assert plan([(11008, 4096)], bits=8, gs=None) == ([4], 4, 2)  # INT8 wants 8192 waves
     # M = 2, launches whose M = 1 plan has one-wave tiles: gemv_mx_pipe_kernel
     # (kind 7) with the M = 1 rows per tile.
