@@ -2576,8 +2576,10 @@ void waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk,
 }
 
 // wk for an M = 1 launch (gemv_m1_pipe_kernel takes those of one-wave
-// tiles): one-wave tiles, in place of the K split above, for every INT2
-// launch and for INT4 / INT8 launches of at most kPipeTiles four-row tiles.
+// tiles): one-wave tiles, in place of the K split above, for INT2 launches
+// and for INT4 / INT8 launches of at most kPipeTiles four-row tiles, from
+// kPipeMinTiles tiles on (smaller launches keep the split: one-wave tiles
+// leave most SIMDs idle there).
 // The pipelined kernel (or an INT2 staged / kept variant) then walks whole
 // rows with the activations staged per block. Measured against the K split
 // (graph replays of distinct weights): INT2 8192 x 28672 (C5 down_proj)
@@ -2587,12 +2589,15 @@ void waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk,
 // 5.10 -> 5.22, C5 o_proj (2048) 9.33 -> 9.7, C5 q|k|v (2560) 10.8 -> 11.8,
 // INT8 11008 x 4096 (C2, 2752 tiles) 9.24 -> 10.32.
 constexpr int64_t kPipeTiles = 1024;
+// INT4 1024 x 4096 (k_proj; 256 tiles) 3.50 us split against 3.81 one-wave,
+// 1024 x 8192 3.88 against 5.36.
+constexpr int64_t kPipeMinTiles = 512;
 
 void m1_waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk) {
   waves_per_tile(ops, count, bits, R, wk);
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i) tiles += (ops[i].N + R - 1) / R;
-  if (bits == 2 || (R == 4 && tiles <= kPipeTiles))
+  if (tiles >= kPipeMinTiles && (bits == 2 || (R == 4 && tiles <= kPipeTiles)))
     for (int i = 0; i < count; ++i) wk[i] = 1;
 }
 

@@ -245,12 +245,14 @@ def test_gemv_plan_geometry():
     # (INT4 and INT8). INT4: 32 codes per 16-byte column. Rows per tile: 8 for
     # launches with >= 6144 tiles of 8 rows, else 4. wk: smallest of 1, 2, 4 giving
     # the launch 6144 waves (INT4), capped so each wave keeps >= 40 columns; but
-    # one-wave tiles for INT2 launches and for launches of at most 1024 tiles.
+    # one-wave tiles for INT2 launches and for launches of 512 to 1024 tiles.
     assert plan([(14336, 4096)]) == ([2], 4, 2)
     assert plan([(14336, 4096)] * 2) == ([1, 1], 4, 4)          # gate | up: 7168 waves already
     assert plan([(4096, 14336)]) == ([1], 4, 4)                 # 1024 tiles: one wave each
     assert plan([(4096, 4096)]) == ([1], 4, 4)
-    assert plan([(1024, 4096)]) == ([1], 4, 4)
+    assert plan([(1024, 4096)]) == ([2], 4, 2)                  # 256 tiles: under 512, the split stays
+    assert plan([(1024, 8192)]) == ([4], 4, 2)
+    assert plan([(2048, 4096)]) == ([1], 4, 4)                  # 512 tiles: one wave each
     assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 2)  # 1536 tiles: split
     assert plan([(4096, 4096), (1024, 4096), (1024, 4096)], bits=8, gs=128) == ([4, 4, 4], 4, 2)
     assert plan([(8192, 8192)]) == ([4], 8, 2)                  # K >= 8192, 1024 tiles of 8 rows: 8-row split
