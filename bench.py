@@ -37,6 +37,13 @@ Measurement protocol (why the timed replays see the steady state):
     ceiling (a measurement of its own, reported below, long enough to cover
     that ramp); the headline stack follows immediately with its W warm-up
     and K timed replays.
+  * The launch-bound legs (C4 decode and per_linear, their read floors, the
+    prologue legs, C5 decode) warm up for at least SETTLE_MS of estimated
+    replay time (their bytes at 4 TB/s), W replays at least: right after the
+    headline's stack leg the same decode graph ran 7% slower (32.9 against
+    30.7 us/layer, its kernels within 1%: the gaps between launches grow),
+    and reached its steady figure after a few hundred ms of launches. The
+    warm-up replays of every leg are in protocol.legs.
   * roofline.achieved is the dominant kernel's own duration: a leg replays
     the stack step five times per graph (70 launches back to back, so the
     per-replay launch overhead is spread thin), and replay time / launches is
@@ -107,6 +114,8 @@ CEILING_BYTES = 4 * 2 ** 30      # streaming-read ceiling buffer
 CEILING_WARM, CEILING_REPS = 20, 40
 EMPTY_LAUNCHES = 1000
 LAUNCH_LEG_STEPS = 5             # stack steps per replay of the launch-duration leg
+SETTLE_MS = 250                  # minimum warm-up of the launch-bound legs (see the protocol above)
+SETTLE_GBS = 4000.0              # the rate that warm-up is estimated at
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "dq_kernels_bench_legs_traffic.md")
 
 # a Llama-3-70B-shape stack in mixed precision
@@ -305,9 +314,12 @@ class Leg:
 
     eager = False
 
-    def __init__(self, torch, name, fn, steps, warmup, step_bytes=None, meta=None, layers=None, launch_bytes=None):
+    def __init__(self, torch, name, fn, steps, warmup, step_bytes=None, meta=None, layers=None, launch_bytes=None,
+                 settle=False):
         self.torch, self.name, self.fn = torch, name, fn
         self.graph = None if Leg.eager else capture(torch, fn)
+        if settle and step_bytes:  # at least SETTLE_MS of replays at the estimated rate
+            warmup = max(warmup, math.ceil(SETTLE_MS * 1e-3 * SETTLE_GBS * 1e9 / step_bytes))
         self.steps, self.warmup = steps, warmup
         self.step_bytes, self.meta, self.layers = step_bytes, meta or {}, layers
         self.launch_bytes = launch_bytes
@@ -335,7 +347,7 @@ class Leg:
         return out
 
 
-def gemv_leg(torch, eng, name, launches, steps, warmup, layers):
+def gemv_leg(torch, eng, name, launches, steps, warmup, layers, settle=False):
     step_bytes = sum(launch_bytes(x, p) for _, x, p in launches)
 
     def fn():
@@ -344,10 +356,11 @@ def gemv_leg(torch, eng, name, launches, steps, warmup, layers):
 
     meta = {"launches_per_step": len(launches),
             "kernel_instances": {k: len(v) for k, v in kernel_instances(eng, launches).items()}}
-    return Leg(torch, name, fn, steps, warmup, step_bytes, meta, layers, [launch_bytes(x, p) for _, x, p in launches])
+    return Leg(torch, name, fn, steps, warmup, step_bytes, meta, layers, [launch_bytes(x, p) for _, x, p in launches],
+               settle=settle)
 
 
-def read_floor_leg(torch, eng, name, flat, sink, sizes, steps, warmup, layers):
+def read_floor_leg(torch, eng, name, flat, sink, sizes, steps, warmup, layers, settle=False):
     """A plain streaming read (stream_read_kernel) of each launch's
     algorithmic bytes, in the same launch structure: consecutive regions of
     `flat` (wrapping at its end), one read launch per GEMV launch."""
@@ -364,7 +377,7 @@ def read_floor_leg(torch, eng, name, flat, sink, sizes, steps, warmup, layers):
             eng.stream_read(v, sink)
 
     return Leg(torch, name, fn, steps, warmup, sum(v.numel() for v in views), layers=layers,
-               launch_bytes=[v.numel() for v in views])
+               launch_bytes=[v.numel() for v in views], settle=settle)
 
 
 def kernel_durations(torch, eng, launches, reps):
@@ -809,14 +822,15 @@ def main():
     if "stack" not in modes:
         modes.insert(0, "stack")
     c4_launches = {mode: step_launches(stack, xs, mode) for mode in modes}
-    legs = {f"C4 {mode}": gemv_leg(torch, eng, mode, c4_launches[mode], args.steps, args.warmup, args.layers)
+    legs = {f"C4 {mode}": gemv_leg(torch, eng, mode, c4_launches[mode], args.steps, args.warmup, args.layers,
+                                   settle=mode != "stack")
             for mode in modes}
     # the floor of each structure: a plain read of every launch's bytes
     flat = ceiling_buf.view(torch.uint8)
     for mode in modes:
         legs[f"read floor {mode}"] = read_floor_leg(torch, eng, f"read floor {mode}", flat, sink,
                                                     legs[f"C4 {mode}"].launch_bytes, args.steps, args.warmup,
-                                                    args.layers)
+                                                    args.layers, settle=mode != "stack")
     # the headline's launch-duration leg: the same step five times in one
     # graph, so the per-replay launch overhead is spread over 70 launches
     legs["C4 stack x5"] = gemv_leg(torch, eng, "stack x5", c4_launches["stack"] * LAUNCH_LEG_STEPS, args.steps,
@@ -832,7 +846,7 @@ def main():
             legs[f"stack M={m}"] = gemv_leg(torch, eng, f"M={m}", step_launches(stack, mxs, "stack"), args.steps,
                                             args.warmup, args.layers)
         legs["prologue plain"] = gemv_leg(torch, eng, "plain", step_launches(stack, xs, "decode"), args.steps,
-                                          args.warmup, args.layers)
+                                          args.warmup, args.layers, settle=True)
 
         def run_fused():
             for li, (layer, x) in enumerate(zip(stack, xs)):
@@ -847,7 +861,7 @@ def main():
         legs["prologue fused"] = Leg(torch, "fused", run_fused, args.steps, args.warmup,
                                      legs["prologue plain"].step_bytes, layers=args.layers,
                                      launch_bytes=[b + extra[i % 4] for i, b in
-                                                   enumerate(legs["prologue plain"].launch_bytes)])
+                                                   enumerate(legs["prologue plain"].launch_bytes)], settle=True)
 
         def rmsnorm(x):  # transformers' LlamaRMSNorm in torch ops
             h = x.float()
@@ -867,9 +881,10 @@ def main():
         # plus the RMSNorm and SwiGLU as torch ops (not counted in its bytes;
         # the leg is timed last, as its kernel count per step is torch's)
         unfused = Leg(torch, "unfused", run_unfused, args.steps, args.warmup, legs["prologue plain"].step_bytes,
-                      layers=args.layers, launch_bytes=legs["prologue plain"].launch_bytes)
+                      layers=args.layers, launch_bytes=legs["prologue plain"].launch_bytes, settle=True)
         for mode, ls in c5_launches(*c5).items():
-            legs[f"C5 {mode}"] = gemv_leg(torch, eng, mode, ls, args.steps, args.warmup, C5_LAYERS)
+            legs[f"C5 {mode}"] = gemv_leg(torch, eng, mode, ls, args.steps, args.warmup, C5_LAYERS,
+                                          settle=mode == "decode")
         for name, n, k, spec, m in SINGLE_CONFIGS:
             pws = singles["C2" if name == "C2_M4" else name]
             x = single_x[name]
