@@ -694,7 +694,7 @@ def counter_pass(torch, args, eng, stack, ceiling, legs):
 def cpu_baseline(torch, c4_layer, singles, c5_layer, budget_s=30.0):
     """The reference's CPU torch path (oracle/cpu_path.py: unpack -> dequantize
     -> fp32 F.linear), timed with time.perf_counter on this host's cores
-    (torch.get_num_threads()) per BASELINE.md's protocol: 3 warm-ups, then the
+    (torch.get_num_threads()): 3 warm-ups, then the
     median and p25/p75 of up to 20 repetitions (fewer for rows whose single
     repetition would overrun the time budget; the count is recorded),
     'dequant + matmul' and 'matmul only' (the fp32 weight materialized
@@ -766,8 +766,8 @@ def cpu_baseline(torch, c4_layer, singles, c5_layer, budget_s=30.0):
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "DESIGN.md describes how the path would shard", file=sys.stderr)
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
         return 2
     import torch
 
