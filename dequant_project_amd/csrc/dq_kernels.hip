@@ -2593,11 +2593,17 @@ constexpr int64_t kPipeTiles = 1024;
 // 1024 x 8192 3.88 against 5.36.
 constexpr int64_t kPipeMinTiles = 512;
 
-void m1_waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk) {
+// RMSNorm launches take one-wave tiles up to kRmsPipeTiles: on the K split
+// every lane of every K share forms x * gamma and sum(x^2) again, where the
+// pipelined kernel does it once per block and batch.
+constexpr int64_t kRmsPipeTiles = 2048;
+
+void m1_waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk,
+                       int64_t max_tiles = kPipeTiles) {
   waves_per_tile(ops, count, bits, R, wk);
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i) tiles += (ops[i].N + R - 1) / R;
-  if (tiles >= kPipeMinTiles && (bits == 2 || (R == 4 && tiles <= kPipeTiles)))
+  if (tiles >= kPipeMinTiles && (bits == 2 || (R == 4 && tiles <= max_tiles)))
     for (int i = 0; i < count; ++i) wk[i] = 1;
 }
 
@@ -2761,7 +2767,7 @@ M1Variant m1_variant(const KernelBatch& kb, int count, int bits, int R, const in
 template <int BITS, bool SYM, bool INTER, int R, int PRO = kProNone>
 hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStream_t stream, float eps = 0.f) {
   int wks[kMaxBatch];
-  m1_waves_per_tile(ops, count, BITS, R, wks);
+  m1_waves_per_tile(ops, count, BITS, R, wks, PRO == kProRmsNorm ? kRmsPipeTiles : kPipeTiles);
   KernelBatch kb;
   const int bts = fill_kernel_batch(ops, count, M, BITS, R, 1, wks, kb);
   kb.eps = eps;

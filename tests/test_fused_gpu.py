@@ -50,10 +50,12 @@ def packed_group(torch, n, k, count, fmt, seed):
 
 
 # (N, K, problems): split-K tiles (one small problem) and full-K tiles (a
-# 16-problem launch), K = 11008 (172 INT2 chunks: a ragged last column), and
-# two problems of one-wave 4-row tiles (the decode step's gate | up shape
-# class: RMSNorm on the pipelined kernel, the prologue staged per block)
-SHAPES = [(256, 4096, 1), (1000, 2048, 3), (4096, 4096, 16), (300, 11008, 2), (12288, 1024, 2)]
+# 16-problem launch), K = 11008 (172 INT2 chunks: a ragged last column), two
+# problems of one-wave 4-row tiles (the decode step's gate | up shape class:
+# RMSNorm on the pipelined kernel, the prologue staged per block), and three
+# problems of 1536 four-row tiles (the q|k|v class: RMSNorm launches of up to
+# 2048 tiles take one-wave tiles too)
+SHAPES = [(256, 4096, 1), (1000, 2048, 3), (4096, 4096, 16), (300, 11008, 2), (12288, 1024, 2), (2048, 4096, 3)]
 
 
 @pytest.mark.parametrize("n,k,count", SHAPES)
