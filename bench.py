@@ -199,9 +199,8 @@ class Engine:
             return f"gemv_mx_pipe_kernel<{fmt}, {rows.value}, 2>", tuple(wk)
         if kind.value == 4:
             return f"gemv_m1_pipe_kernel<{fmt}, {rows.value}>", tuple(wk)
-        if kind.value in (5, 6):
-            xm = "staged x" if kind.value == 5 else "kept x"
-            return f"gemv_m1_kernel<{fmt}, {rows.value}, false> ({xm})", tuple(wk)
+        if kind.value == 6:
+            return f"gemv_m1_kernel<{fmt}, {rows.value}, false> (kept x)", tuple(wk)
         return f"gemv_m1_kernel<{fmt}, {rows.value}, {'true' if kind.value == 3 else 'false'}>", tuple(wk)
 
     def stream(self):

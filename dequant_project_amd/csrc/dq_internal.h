@@ -35,7 +35,7 @@ void set_launch_events(hipEvent_t start, hipEvent_t stop);
 // *mfma == 2: gemv_m1_kernel<bits, sym, inter, rows, false> (M = 1, VALU dots);
 // *mfma == 3: gemv_m1_kernel<bits, sym, inter, rows, true> (M = 1, MFMA dots);
 // *mfma == 4: gemv_m1_pipe_kernel<bits, sym, inter, rows> (M = 1, pipelined walk);
-// *mfma == 5 / 6: gemv_m1_kernel's INT2 staged / kept-activation variants (M = 1);
+// *mfma == 6: gemv_m1_kernel's INT2 kept-activation variant (M = 1);
 // *mfma == 7: gemv_mx_pipe_kernel<bits, sym, inter, rows, 2> (M = 2, one-wave tiles).
 void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows, int* mfma);
 

@@ -733,91 +733,30 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Activations of one M = 1 batch staged in LDS for the whole block (kXmStage):
-// the 64 chunk columns of the batch, one padded 16-byte-aligned slot per
-// chunk (a lane's reads then spread over the banks). Used when every tile of
-// the launch is one wave wide (wk = 1), so the block's four waves walk the
-// same chunk columns in step: one coalesced load per block instead of one per
-// wave (INT2 carries as many activation bytes per lane as weight bytes).
-template <int BITS>
-struct XStage {
-  static constexpr int kChunkBytes = Fmt<BITS>::CPL * 2;
-  static constexpr int kPieces = kChunkBytes / 16;
-  static constexpr int kStride = kChunkBytes + 16;
-  static constexpr int kBufBytes = 64 * kStride;
-  static constexpr int kPerThread = (64 * kPieces + kGemvThreads - 1) / kGemvThreads;
-};
-
-template <int BITS>
-__device__ __forceinline__ void xstage_issue(const KernelProblem& d, const TilePos& tb,
-                                             u32x4 (&st)[XStage<BITS>::kPerThread]) {
-  using XS = XStage<BITS>;
-  const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(d.K) * 2u);
-#pragma unroll
-  for (int i = 0; i < XS::kPerThread; ++i) {
-    const int e = static_cast<int>(threadIdx.x) + kGemvThreads * i;
-    const int cc = e / XS::kPieces, pc = e % XS::kPieces;
-    const int c = tb.cb + cc;
-    st[i] = __builtin_amdgcn_raw_buffer_load_b128(
-        xbuf, e < 64 * XS::kPieces && c < tb.ce ? static_cast<uint32_t>(c) * XS::kChunkBytes + 16u * pc : kOutOfRange,
-        0, 0);
-  }
-}
-
-template <int BITS>
-__device__ __forceinline__ void xstage_write(unsigned char* buf, const u32x4 (&st)[XStage<BITS>::kPerThread]) {
-  using XS = XStage<BITS>;
-#pragma unroll
-  for (int i = 0; i < XS::kPerThread; ++i) {
-    const int e = static_cast<int>(threadIdx.x) + kGemvThreads * i;
-    if (e < 64 * XS::kPieces)
-      *reinterpret_cast<u32x4*>(buf + (e / XS::kPieces) * XS::kStride + 16 * (e % XS::kPieces)) = st[i];
-  }
-}
-
-template <int BITS, bool INTER>
-__device__ __forceinline__ void xstage_read(const unsigned char* buf, int lane, h2 (&xr)[4][Fmt<BITS>::PAIRS]) {
-  using F = Fmt<BITS>;
-  using XS = XStage<BITS>;
-  uint32_t xd[F::CPL / 2];
-#pragma unroll
-  for (int k = 0; k < XS::kPieces; ++k) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(buf + lane * XS::kStride + 16 * k);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) xd[4 * k + e] = v[e];
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xr[j]);
-}
-
 // Where an M = 1 launch's activations come from (gemv_m1_kernel's XM):
 //   kXmLoad   every wave loads each batch's activations;
-//   kXmStage  the block stages each batch's activations once in LDS (XStage);
 //   kXmKeep   tiles of one batch, each block walking a contiguous range of
 //             block-tiles: a wave keeps the activation pairs of its last tile
 //             in its own LDS slot (8 KiB for INT2) and their bias sums in
 //             registers, and loads x again only when a tile reads other
 //             columns or another x (the q | k | v and gate | up problems of a
 //             layer share x, so most tiles of a long range reuse them).
-enum : int { kXmLoad = 0, kXmStage = 1, kXmKeep = 2 };
+enum : int { kXmLoad = 0, kXmKeep = 2 };
 
 template <int BITS, bool SYM, bool INTER, int R, bool MF, int PRO, int XM>
 __global__ void __launch_bounds__(kGemvThreads)
 gemv_m1_kernel(const KernelBatch b) {
   using F = Fmt<BITS>;
-  constexpr bool XL = XM == kXmStage;
   constexpr bool KEEP = XM == kXmKeep;
   static_assert(!KEEP || (PRO == kProNone && !MF), "kept activations: plain VALU launches");
   constexpr int PW = PRO == kProRmsNorm ? R + 1 : R;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   __shared__ float part[2][kWavesPerBlock][PW];
-  __shared__ __align__(16) unsigned char xl[XL ? 2 * XStage<BITS>::kBufBytes : 16];
   ClassMagics<BITS> cm;
   cm.init();
   const int total = b.bt_start[b.count];
   int phase = 0;
-  int parity = 0;  // XL: staging buffer of the next batch, across tiles
   int p = 0;
   // block-tiles in runs of `run` consecutive ones, the runs strided over the
   // grid: run = 1 is the plain grid-stride walk. KEEP walks runs of b.run
@@ -842,9 +781,7 @@ gemv_m1_kernel(const KernelBatch b) {
 #pragma unroll
     for (int r = 0; r < R; ++r) yacc[r] = 0.f;
     float ssq = 0.f;  // RMSNorm prologue: this wave's sum(x^2)
-    // XL: every wave of the block, active or not, walks the batches (they
-    // stage the activations together and meet at each batch's barrier)
-    if (XL || t.active) {
+    if (t.active) {
       for (int cbase = t.cb; cbase < t.ce; cbase += 64) {
         TilePos tb = t;
         tb.cb = cbase;
@@ -855,17 +792,7 @@ gemv_m1_kernel(const KernelBatch b) {
         h2 xr[1][4][F::PAIRS];
         XRaw<BITS, PRO> raw;
         TileLoads<BITS, R, 1> L;
-        if constexpr (XL) {
-          unsigned char* buf = xl + parity * XStage<BITS>::kBufBytes;
-          parity ^= 1;
-          u32x4 st[XStage<BITS>::kPerThread];
-          xstage_issue<BITS>(d, tb, st);
-          if (t.active) issue_tile_m1<BITS, SYM, R>(d, tb, lane, L);
-          __builtin_amdgcn_sched_barrier(0);
-          xstage_write<BITS>(buf, st);
-          lds_barrier();  // the weights stay in flight
-          xstage_read<BITS, INTER>(buf, lane, xr[0]);
-        } else if constexpr (KEEP) {
+        if constexpr (KEEP) {
           // the tile's one batch (tb == t); a fresh load keeps the order of
           // the path below (activations first), the pairs replace the kept ones
           u32x4* kept = xkeep + wave * F::PAIRS * 64;  // piece q of lane l at q * 64 + l
@@ -909,17 +836,15 @@ gemv_m1_kernel(const KernelBatch b) {
           __builtin_amdgcn_sched_barrier(0);
           if constexpr (PRO != kProNone) x_pairs_pro<BITS, INTER, PRO>(raw, xr[0], ssq);
         }
-        if (t.active) {
-          float acc[R];
+        float acc[R];
 #pragma unroll
-          for (int r = 0; r < R; ++r) acc[r] = 0.f;
-          if constexpr (KEEP)
-            tile_math_m1_sums<BITS, SYM, R, MF>(L, xr[0], Sk, Ck, cm, lane, acc);
-          else
-            tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr[0], cm, lane, acc);
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+        if constexpr (KEEP)
+          tile_math_m1_sums<BITS, SYM, R, MF>(L, xr[0], Sk, Ck, cm, lane, acc);
+        else
+          tile_math_m1<BITS, SYM, INTER, R, MF>(L, xr[0], cm, lane, acc);
 #pragma unroll
-          for (int r = 0; r < R; ++r) yacc[r] += acc[r];
-        }
+        for (int r = 0; r < R; ++r) yacc[r] += acc[r];
       }
     }
     if constexpr (PRO == kProRmsNorm)
@@ -2580,7 +2505,7 @@ void waves_per_tile(const GemvOperand* ops, int count, int bits, int R, int* wk,
 // and for INT4 / INT8 launches of at most kPipeTiles four-row tiles, from
 // kPipeMinTiles tiles on (smaller launches keep the split: one-wave tiles
 // leave most SIMDs idle there).
-// The pipelined kernel (or an INT2 staged / kept variant) then walks whole
+// The pipelined kernel (or the INT2 kept variant) then walks whole
 // rows with the activations staged per block. Measured against the K split
 // (graph replays of distinct weights): INT2 8192 x 28672 (C5 down_proj)
 // 24.1 -> 16.9 us, 4096 x 14336 8.57 -> 7.52, 4096 x 11008 (C3) 7.39 ->
@@ -2696,22 +2621,6 @@ int fill_kernel_batch(const GemvOperand* ops, int count, int64_t M, int bits, in
   return bts;
 }
 
-// Activations staged per block in LDS (gemv_m1_kernel<..., kXmStage>) for
-// INT2, whose lanes load as many activation bytes as weight bytes, in
-// launches where every tile is one wave wide, a tile holds at least two
-// batches (K >= 8192) and the persistent grid walks at least xl_rounds(R)
-// rounds of block-tiles. Measured: C5 stack (K = 8192 / 28672 MLP) +7%;
-// K = 4096 tiles of one batch no change; the same staging on every
-// multi-round INT4 launch: INT4 stack -2.6%. The rounds floor was 4 while the
-// 8-row variant held three waves per SIMD (a 2.3-round decode launch then
-// lost 4%); it now holds four, as the unstaged kernel does. A floor of 2
-// took the C4 INT2 stack's two-round K = 14336 launches too (+2.2% on that
-// stack), one of 1 also C5 decode's 1.75-round gate | up launches (C5 decode
-// +3.5%). The 4-row variant still holds one wave per SIMD fewer than its
-// unstaged kernel and keeps the floor of 4.
-constexpr bool m1_stages_x(int bits) { return bits == 2; }
-constexpr int xl_rounds(int R) { return R == 8 ? 1 : 4; }
-
 // Activations kept across tiles (gemv_m1_kernel<..., kXmKeep>) for INT2
 // launches of 8-row, one-batch tiles (K <= 4096, one wave per tile) of at
 // least kKeepRounds rounds of block-tiles: the grid walks runs of kKeepRun
@@ -2729,33 +2638,29 @@ constexpr int kKeepRun = 3;
 constexpr int kKeepRounds = 2;
 
 // Which M = 1 kernel variant a launch runs (PRO = none; of the prologue
-// launches, RMSNorm ones of one-wave tiles take gemv_m1_pipe_kernel with the
+// launches, those of one-wave tiles take gemv_m1_pipe_kernel with the
 // prologue, the others gemv_m1_kernel's load variant):
-//   kM1Stage  INT2, activations staged per block (conditions above), needs
-//             at least xl_rounds(R) rounds of its grid;
 //   kM1Keep   INT2, 8-row one-batch tiles, activations kept across tiles,
 //             needs kKeepRounds rounds of its grid;
 //   kM1Pipe   gemv_m1_pipe_kernel: every other launch of one-wave tiles
 //             (wk = 1 for every problem, so its walk has no barrier). On the
-//             INT2 launches outside the two variants above (the C4 decode
-//             gate | up launch: 4-row tiles) it measured 13% faster than the
-//             load variant (C4 INT2 decode 1.04 -> 0.905 ms/step); on the
-//             INT2 stack it ties the staged/kept variants, which keep those
-//             launches;
+//             INT2 launches outside the kept variant it measured 13% faster
+//             than the load variant (C4 INT2 decode 1.04 -> 0.905 ms/step),
+//             and faster than a block-staged variant of gemv_m1_kernel (one
+//             coalesced activation load per block and batch) that took the
+//             INT2 launches of K >= 8192 before: C5 stack 54.7 -> 51.4
+//             us/layer, C4 INT2 stack 14.79 -> 14.38 us/layer, C5 decode
+//             5.386 -> 5.362 ms/step (that variant was then removed); on the
+//             INT2 stack it ties the kept variant;
 //   kM1Load   gemv_m1_kernel, activations loaded per wave (split-K launches).
-// grid_stage / grid_keep: the co-resident blocks of the staged / kept kernels.
-enum M1Variant : int { kM1Load = 2, kM1Pipe = 4, kM1Stage = 5, kM1Keep = 6 };
+// Kind 5 of dq_gemv_plan (the block-staged variant) is no longer returned.
+// grid_keep: the co-resident blocks of the kept kernel.
+enum M1Variant : int { kM1Load = 2, kM1Pipe = 4, kM1Keep = 6 };
 
-M1Variant m1_variant(const KernelBatch& kb, int count, int bits, int R, const int* wks, int bts, int grid_stage,
-                     int grid_keep) {
+M1Variant m1_variant(const KernelBatch& kb, int count, int bits, int R, const int* wks, int bts, int grid_keep) {
   bool one_wave = true;
   for (int i = 0; i < count; ++i) one_wave = one_wave && wks[i] == 1;
   if (!one_wave) return kM1Load;
-  if (m1_stages_x(bits)) {
-    bool stage = true;
-    for (int i = 0; i < count; ++i) stage = stage && kb.p[i].n_chunks >= 2 * 64;
-    if (stage && bts >= xl_rounds(R) * grid_stage) return kM1Stage;
-  }
   if (m1_keeps_x(bits) && R == 8) {
     bool keep = true;
     for (int i = 0; i < count; ++i) keep = keep && kb.p[i].n_chunks <= 64;
@@ -2773,14 +2678,9 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
   kb.eps = eps;
   if (bts == 0) return hipSuccess;
   if constexpr (PRO == kProNone && !m1_uses_mfma(BITS)) {
-    constexpr auto stage_kernel = gemv_m1_kernel<BITS, SYM, INTER, R, false, PRO, kXmStage>;
     constexpr auto keep_kernel = gemv_m1_kernel<BITS, SYM, INTER, R, false, PRO, kXmKeep>;
-    const int grid_stage = m1_stages_x(BITS) ? resident_blocks<stage_kernel>() : 0;
     const int grid_keep = m1_keeps_x(BITS) && R == 8 ? resident_blocks<keep_kernel>() : 0;
-    switch (m1_variant(kb, count, BITS, R, wks, bts, grid_stage, grid_keep)) {
-      case kM1Stage:
-        if constexpr (m1_stages_x(BITS)) return launch_kernel(stage_kernel, grid_stage, kb, stream);
-        break;
+    switch (m1_variant(kb, count, BITS, R, wks, bts, grid_keep)) {
       case kM1Keep:
         if constexpr (m1_keeps_x(BITS) && R == 8) {
           kb.run = kKeepRun;
@@ -3173,7 +3073,7 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
   if (M == 1) m1_waves_per_tile(ops, count, bits, *rows, wk);
   else waves_per_tile(ops, count, bits, *rows, wk);
   if (M == 1 && !m1_uses_mfma(bits)) {
-    // the INT2 staged / kept variants hold four blocks per CU; the launch
+    // the INT2 kept variant holds four blocks per CU; the launch
     // itself asks the device for its kernel's co-resident blocks
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -3183,7 +3083,7 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
     }
     KernelBatch kb;
     const int bts = fill_kernel_batch(ops, count, M, bits, *rows, 1, wk, kb);
-    *mfma = m1_variant(kb, count, bits, *rows, wk, bts, 4 * cus, 4 * cus);
+    *mfma = m1_variant(kb, count, bits, *rows, wk, bts, 4 * cus);
   }
 }
 

@@ -242,9 +242,6 @@ int dq_gemm_small_plan(const dq_gemv_problem* problems, int count, int64_t M, in
  *                      rows_per_tile> (M = 1, launches whose tiles are all
  *                      one wave wide: the next batch's loads are issued while
  *                      the current batch is computed),
- *   *kernel_kind == 5: gemv_m1_kernel's INT2 variant that stages each batch's
- *                      activations per block in LDS (one-wave tiles, K >= 8192,
- *                      enough rounds of its persistent grid),
  *   *kernel_kind == 6: gemv_m1_kernel's INT2 variant that keeps a wave's
  *                      activations across consecutive 8-row one-batch tiles
  *                      (K <= 4096, at least two rounds of its grid),
@@ -252,8 +249,9 @@ int dq_gemm_small_plan(const dq_gemv_problem* problems, int count, int64_t M, in
  *                      rows_per_tile, 2> (M = 2, launches whose tiles are
  *                      all one wave wide: kind 4's walk with each weight
  *                      chunk dotted with both batch rows).
- * Kinds 5 and 6 depend on the device's co-resident blocks; without a device
- * the plan assumes 256 CUs.
+ * Kind 6 depends on the device's co-resident blocks; without a device the
+ * plan assumes 256 CUs. (Kind 5, a block-staged INT2 variant, is no longer
+ * returned: the pipelined kernel of kind 4 measured faster on its launches.)
  * The geometry is chosen per launch, so a problem's result is deterministic
  * for a given launch but may differ in the last bits between a grouped launch
  * and a single one. waves_per_tile must hold `count` ints. */

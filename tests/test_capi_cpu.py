@@ -262,7 +262,7 @@ def test_gemv_plan_geometry():
     assert plan([(4096, 14336)] * 16) == ([1] * 16, 8, 4)
     assert plan([(4096, 14336)] * 16, bits=8, gs=None) == ([1] * 16, 8, 4)
     assert plan([(14336, 4096)] * 16, bits=2, gs=64) == ([1] * 16, 8, 6)  # INT2: activations kept across tiles
-    assert plan([(14336, 8192)] * 16, bits=2, gs=64) == ([1] * 16, 8, 5)  # INT2: activations staged per block
+    assert plan([(14336, 8192)] * 16, bits=2, gs=64) == ([1] * 16, 8, 4)  # INT2 K = 8192: pipelined
     assert plan([(14336, 4096)] * 2, bits=2, gs=64) == ([1, 1], 4, 4)     # INT2 decode gate | up: pipelined
     assert plan([(4096, 11008)], bits=2, gs=64) == ([1], 4, 4)  # INT2: one-wave tiles, pipelined
     assert plan([(8192, 28672)], bits=2, gs=64) == ([1], 8, 4)

@@ -652,22 +652,21 @@ def test_grouped_launch_sixteen_problems_and_python_api(torch_gpu):
     (2, 64, False, 8000, 14336, 6),    # R = 4 tiles, 224 chunks per row (3.5 batches)
     (8, None, True, 8000, 4096, 10),   # per-channel INT8
     (2, 64, False, 4093, 4096, 16),    # INT2 rows under 8192 codes, last 8-row tile partial
-    (2, 64, False, 28672, 8192, 2),    # INT2 staged per block at under two rounds (the C5
+    (2, 64, False, 28672, 8192, 2),    # INT2 pipelined at under two rounds (the C5
                                        # gate | up launch: 1792 block-tiles)
-    (2, 64, False, 8165, 8192, 16),    # INT2 with activations staged per block in LDS:
-                                       # 4084 block-tiles of two batches, ~4 rounds; each
-                                       # problem's last block-tile holds one 5-row tile and
-                                       # three waves that only stage
+    (2, 64, False, 8165, 8192, 16),    # INT2 pipelined over 4084 block-tiles of two
+                                       # batches, ~4 rounds; each problem's last
+                                       # block-tile holds one 5-row tile and three
+                                       # waves that only stage activations
 ])
 def test_grouped_launch_over_several_rounds(torch_gpu, bits, gs, sym, n, k, count):
     """M = 1 launches with more block-tiles than the persistent grid holds
     (1792-4096 block-tiles against at most ~2000 resident blocks), so blocks
-    walk several rounds and cross problem boundaries mid-walk; the last case
-    is large enough (every tile one wave wide, two batches per tile, about
-    four rounds of the 1024-block grid) for the INT2 kernel that stages the
-    activations per block in LDS. Every problem against the oracle on a sample
-    of rows that includes each problem's last 40 rows, and against its single
-    call (which, 64 times smaller, runs the unstaged kernel)."""
+    walk several rounds and cross problem boundaries mid-walk; the INT2 cases
+    of K = 8192 (every tile one wave wide, two batches per tile) run the
+    pipelined walk over up to about four rounds of its grid. Every problem
+    against the oracle on a sample of rows that includes each problem's last
+    40 rows, and against its single call (a launch of its own geometry)."""
     torch = torch_gpu
     from dequant_project_amd.packer import QuantConfig, quantize_tensor
 
