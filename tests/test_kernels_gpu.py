@@ -938,3 +938,37 @@ def test_weights_past_two_gib_run_as_row_slices(torch_gpu, m):
     print(f"2.29 GB INT8 weight M={m}: worst={worst:.3f}x tol rel_l2={P.rel_l2(y, ref):.2e}", flush=True)
     assert ok, f"elementwise criterion violated, worst {worst:.3f}x"
     assert P.rel_l2(y, ref) <= REL_L2_TOL
+
+
+@pytest.mark.parametrize("bits,gs,sym,n,k,plan", [
+    (4, 128, False, 2044, 4096, ([2], 4, 2)),   # 511 four-row tiles: the K split stays
+    (4, 128, False, 2048, 4096, ([1], 4, 4)),   # 512: one-wave tiles, pipelined
+    (4, 128, False, 4096, 4096, ([1], 4, 4)),   # 1024: the last one-wave size
+    (4, 128, False, 4100, 4096, ([2], 4, 2)),   # 1025: the K split again
+    (4, 128, False, 8184, 8192, ([4], 4, 2)),   # K = 8192, 1023 eight-row tiles: four-row split
+    (4, 128, False, 8192, 8192, ([4], 8, 2)),   # 1024 eight-row tiles: eight-row split
+    (2, 64, False, 2044, 14336, ([4], 4, 2)),   # INT2 under 512 tiles: split
+    (2, 64, False, 2048, 14336, ([1], 4, 4)),   # INT2 from 512 tiles: pipelined
+    (8, None, True, 4096, 4096, ([1], 4, 4)),   # INT8 per-channel, 1024 tiles
+    (8, None, True, 4100, 4096, ([4], 4, 2)),
+])
+def test_launch_geometry_thresholds(torch_gpu, bits, gs, sym, n, k, plan):
+    """M = 1 launches on both sides of each geometry threshold (one-wave tiles
+    for 512..1024 four-row tiles and for INT2 from 512 tiles, eight-row
+    tiles for 1024+ of them at K >= 8192): the plan the launch takes, and its
+    output against the oracle on a sample of rows that includes the last 40."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    assert _plan([(n, k)], bits, gs) == plan
+    gen = torch.Generator(device="cuda").manual_seed(n + k + bits)
+    pw = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02,
+                         QuantConfig(bits, gs, sym, "sequential"))
+    rng = np.random.Generator(np.random.PCG64(n))
+    rows = np.unique(np.concatenate([rng.choice(n - 40, 160, replace=False), np.arange(n - 40, n)]))
+    qw, sc = pw.qweight.cpu().numpy(), pw.scales.cpu().numpy()
+    ze = None if pw.zeros is None else pw.zeros.cpu().numpy()
+    case = OracleCase(pw, qw, sc, ze, rows, deq_ref=False)
+    x16 = activations(1, k, seed=n + 3)
+    y = ext().gemv(to_gpu(torch, x16), *ext_args(pw))
+    case.check(y.cpu().numpy(), x16, f"INT{bits} [{n},{k}] plan {plan}")
