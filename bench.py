@@ -199,6 +199,8 @@ class Engine:
             return f"gemv_mx_pipe_kernel<{fmt}, {rows.value}, 2>", tuple(wk)
         if kind.value == 4:
             return f"gemv_m1_pipe_kernel<{fmt}, {rows.value}>", tuple(wk)
+        if kind.value == 8:
+            return f"gemv_m1_pipe_split_kernel<{fmt}, {rows.value}, {wk[0]}>", tuple(wk)
         if kind.value == 6:
             return f"gemv_m1_kernel<{fmt}, {rows.value}, false> (kept x)", tuple(wk)
         return f"gemv_m1_kernel<{fmt}, {rows.value}, {'true' if kind.value == 3 else 'false'}>", tuple(wk)

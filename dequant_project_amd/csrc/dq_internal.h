@@ -36,7 +36,8 @@ void set_launch_events(hipEvent_t start, hipEvent_t stop);
 // *mfma == 3: gemv_m1_kernel<bits, sym, inter, rows, true> (M = 1, MFMA dots);
 // *mfma == 4: gemv_m1_pipe_kernel<bits, sym, inter, rows> (M = 1, pipelined walk);
 // *mfma == 6: gemv_m1_kernel's INT2 kept-activation variant (M = 1);
-// *mfma == 7: gemv_mx_pipe_kernel<bits, sym, inter, rows, 2> (M = 2, one-wave tiles).
+// *mfma == 7: gemv_mx_pipe_kernel<bits, sym, inter, rows, 2> (M = 2, one-wave tiles);
+// *mfma == 8: gemv_m1_pipe_split_kernel<bits, sym, inter, rows, wk> (M = 1, split K).
 void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int* wk, int* rows, int* mfma);
 
 // All problems of one launch share M and the format (bits, symmetry, layout).

@@ -1141,6 +1141,129 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
   }
 }
 
+// gemv_m1_pipe_kernel's walk for launches that split K over WK = 2 or 4
+// waves per tile (no prologue): a block-tile holds 4 / WK tiles, wave w
+// takes share w % WK of tile w / WK, and every share of a block-tile has
+// the same ceil(per_wave / 64) batches (a shorter last share loads zeros
+// past its end). The block stages each batch's activations of all WK
+// shares (WK words per thread, WK buffers per parity); each wave reads its
+// share's buffer, so the activations are loaded once per block, not once per
+// lane as in gemv_m1_kernel's split launches. At a tile's end the shares'
+// sums meet in LDS (double-buffered by tile, an LDS-only barrier: the next
+// batch's rows stay in flight) and share 0 adds them in share order and
+// stores.
+template <int BITS, bool SYM, bool INTER, int R, int WK>
+__global__ void __launch_bounds__(kGemvThreads)
+gemv_m1_pipe_split_kernel(const KernelBatch b) {
+  static_assert(WK == 2 || WK == 4, "K shares per tile");
+  using F = Fmt<BITS>;
+  using PS = PairStage<BITS>;
+  constexpr int Q = R / 4;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  __shared__ __align__(16) unsigned char xs[2 * WK * PS::kBufBytes];
+  __shared__ float part[2][kWavesPerBlock][R];
+  ClassMagics<BITS> cm;
+  cm.init();
+  const int total = b.bt_start[b.count];
+  int p = 0;
+  int bt = static_cast<int>(blockIdx.x);
+  if (bt >= total) return;  // block-uniform: the whole block leaves
+  TilePos t = locate(b, bt, wave, R, p);
+  int j = 0;  // batch of the current tile (block-uniform)
+  int par = 0, phase = 0;
+  BatchAddr<R> a;
+  uint32_t raw[WK][PS::kWordDwords];
+  uint32_t z[R], s[R];
+  u32x4 w[R];
+  // share sh's word of batch jj of problem d (all threads of the block)
+  const auto stage_issue = [&](const KernelProblem& d, int jj, bool live) {
+#pragma unroll
+    for (int sh = 0; sh < WK; ++sh) {
+      const int c0 = sh * d.per_wave;
+      pair_stage_issue<BITS>(d.x, d, c0 + 64 * jj, min(d.n_chunks, c0 + d.per_wave), live, raw[sh]);
+    }
+  };
+  const auto stage_write = [&](int pa) {
+#pragma unroll
+    for (int sh = 0; sh < WK; ++sh) pair_stage_write<BITS, INTER>(xs + (pa * WK + sh) * PS::kBufBytes, raw[sh]);
+  };
+  // the first batch: activations staged, rows in flight
+  stage_issue(b.p[t.p], 0, true);
+  batch_addr<BITS, SYM, R>(b.p[t.p], t.row0, t.cb, t.ce, lane, t.active, a);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    issue_row<SYM, R>(a, r, z[r], s[r], w[r]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  stage_write(0);
+  lds_barrier();
+  float yacc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) yacc[r] = 0.f;
+  for (;;) {
+    // where the next batch is: batch j + 1 of this tile, or the first batch
+    // of the next block-tile (the same for the whole block)
+    const int nb = (b.p[t.p].per_wave + 63) >> 6;
+    int nj = j + 1, nbt = bt, np = p;
+    TilePos nt = t;
+    const bool tile_end = nj >= nb;
+    if (tile_end) {
+      nj = 0;
+      nbt = bt + static_cast<int>(gridDim.x);
+      if (nbt < total) nt = locate(b, nbt, wave, R, np);
+    }
+    const bool nvalid = nbt < total;  // block-uniform
+    h2 xr[4][F::PAIRS];
+    pair_stage_read<BITS>(xs + (par * WK + t.kw) * PS::kBufBytes, lane, xr);
+    float S, C;
+    bias_sums<BITS>(xr, S, C);
+    if constexpr (SYM) C = __builtin_fmaf(static_cast<float>(F::BIAS), S, C);
+    stage_issue(b.p[np], nj, nvalid);
+    batch_addr<BITS, SYM, R>(b.p[np], nt.row0, nt.cb + 64 * nj, nt.ce, lane, nvalid && nt.active, a);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float corr = SYM ? C : __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(z[r])), S, C);
+      const float v = biased_dot_m1<BITS, false>(w[r], xr, cm, lane) - corr;
+      yacc[r] = __builtin_fmaf(f16_to_f32(static_cast<uint16_t>(s[r])), v, yacc[r]);
+      issue_row<SYM, R>(a, r, z[r], s[r], w[r]);  // row r of the next batch
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (tile_end) {
+      wave_sum_rows<R>(yacc);
+      const int g = lane >> 4;
+      if ((lane & 15) == 15) {
+#pragma unroll
+        for (int i = 0; i < Q; ++i) part[phase][wave][g * Q + i] = yacc[i];
+      }
+      lds_barrier();  // every wave of the block ends its tile here
+      if (t.active && t.kw == 0 && (lane & 15) == 15) {
+        float o[Q];
+#pragma unroll
+        for (int i = 0; i < Q; ++i) {
+          float v = 0.f;
+#pragma unroll
+          for (int sh = 0; sh < WK; ++sh) v += part[phase][wave + sh][g * Q + i];
+          o[i] = v;
+        }
+        store_rows<Q>(b.p[t.p].y, t.row0 + g * Q, b.p[t.p].N, o);
+      }
+      phase ^= 1;
+#pragma unroll
+      for (int r = 0; r < R; ++r) yacc[r] = 0.f;
+    }
+    if (!nvalid) break;
+    par ^= 1;
+    stage_write(par);
+    lds_barrier();  // the other buffer was read before the previous barrier
+    j = nj;
+    bt = nbt;
+    p = np;
+    t = nt;
+  }
+}
+
 // Batches of 2 <= M <= MX rows (the launcher uses MX = 2) on gemv_m1_pipe_kernel's walk:
 // each weight row's biased pairs are formed once per chunk and dotted with
 // every batch row's activations (v_dot2, one fp32 chain per row and batch
@@ -2655,6 +2778,23 @@ constexpr int kKeepRounds = 2;
 //   kM1Load   gemv_m1_kernel, activations loaded per wave (split-K launches).
 // Kind 5 of dq_gemv_plan (the block-staged variant) is no longer returned.
 // grid_keep: the co-resident blocks of the kept kernel.
+//
+// Of the split launches, INT4 / INT8 ones of four-row tiles whose K shares
+// are the same 2 or 4 waves in every problem, at most kPipeSplitBlockTiles
+// block-tiles (4096 waves), take gemv_m1_pipe_split_kernel (kind 8 of
+// dq_gemv_plan). Measured against gemv_m1_kernel (graph replays of distinct
+// weights, same box): INT4 1024 x 4096 (k_proj alone, 256 tiles x 2) 3.45 ->
+// 3.20 us, 1024 x 8192 (x 4) 3.86 -> 3.63, C4 q|k|v (1536 x 2) 5.11 -> 5.03;
+// larger launches lost (14336 x 4096, 3584 x 2: 8.15 -> 8.65 us; 11008 x
+// 4096 7.10 -> 7.4; eight-row tiles x 4 on C5 q|k|v 10.4 -> 11.2).
+constexpr int kPipeSplitBlockTiles = 1024;
+
+bool pipe_split(int bits, int R, const int* wks, int count, int bts) {
+  if (bits == 2 || R != 4 || bts > kPipeSplitBlockTiles) return false;
+  for (int i = 1; i < count; ++i)
+    if (wks[i] != wks[0]) return false;
+  return wks[0] == 2 || wks[0] == 4;
+}
 enum M1Variant : int { kM1Load = 2, kM1Pipe = 4, kM1Keep = 6 };
 
 M1Variant m1_variant(const KernelBatch& kb, int count, int bits, int R, const int* wks, int bts, int grid_keep) {
@@ -2692,6 +2832,16 @@ hipError_t launch_gemv_m1(const GemvOperand* ops, int count, int64_t M, hipStrea
         return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
       }
       default:
+        if constexpr (R == 4 && BITS != 2) {
+          if (pipe_split(BITS, R, wks, count, bts)) {
+            if (wks[0] == 2) {
+              constexpr auto kernel = gemv_m1_pipe_split_kernel<BITS, SYM, INTER, R, 2>;
+              return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+            }
+            constexpr auto kernel = gemv_m1_pipe_split_kernel<BITS, SYM, INTER, R, 4>;
+            return launch_kernel(kernel, std::min(bts, resident_blocks<kernel>()), kb, stream);
+          }
+        }
         break;
     }
   }
@@ -3084,6 +3234,7 @@ void plan_gemv_batch(const GemvOperand* ops, int count, int64_t M, int bits, int
     KernelBatch kb;
     const int bts = fill_kernel_batch(ops, count, M, bits, *rows, 1, wk, kb);
     *mfma = m1_variant(kb, count, bits, *rows, wk, bts, 4 * cus);
+    if (*mfma == kM1Load && pipe_split(bits, *rows, wk, count, bts)) *mfma = 8;
   }
 }
 

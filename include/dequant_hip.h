@@ -248,7 +248,12 @@ int dq_gemm_small_plan(const dq_gemv_problem* problems, int count, int64_t M, in
  *   *kernel_kind == 7: gemv_mx_pipe_kernel<bits, symmetric, interleaved,
  *                      rows_per_tile, 2> (M = 2, launches whose tiles are
  *                      all one wave wide: kind 4's walk with each weight
- *                      chunk dotted with both batch rows).
+ *                      chunk dotted with both batch rows),
+ *   *kernel_kind == 8: gemv_m1_pipe_split_kernel<bits, symmetric,
+ *                      interleaved, rows_per_tile, waves_per_tile> (M = 1,
+ *                      INT4 / INT8 launches of 4-row tiles whose K is split
+ *                      over the same 2 or 4 waves in every problem, at most
+ *                      1024 block-tiles: kind 4's walk over the K shares).
  * Kind 6 depends on the device's co-resident blocks; without a device the
  * plan assumes 256 CUs. (Kind 5, a block-staged INT2 variant, is no longer
  * returned: the pipelined kernel of kind 4 measured faster on its launches.)

@@ -250,11 +250,11 @@ def test_gemv_plan_geometry():
     assert plan([(14336, 4096)] * 2) == ([1, 1], 4, 4)          # gate | up: 7168 waves already
     assert plan([(4096, 14336)]) == ([1], 4, 4)                 # 1024 tiles: one wave each
     assert plan([(4096, 4096)]) == ([1], 4, 4)
-    assert plan([(1024, 4096)]) == ([2], 4, 2)                  # 256 tiles: under 512, the split stays
-    assert plan([(1024, 8192)]) == ([4], 4, 2)
+    assert plan([(1024, 4096)]) == ([2], 4, 8)                  # 256 tiles: under 512, the split stays
+    assert plan([(1024, 8192)]) == ([4], 4, 8)                  # (pipelined split walk: kind 8)
     assert plan([(2048, 4096)]) == ([1], 4, 4)                  # 512 tiles: one wave each
-    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 2)  # 1536 tiles: split
-    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)], bits=8, gs=128) == ([4, 4, 4], 4, 2)
+    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)]) == ([2, 2, 2], 4, 8)  # 1536 tiles: split
+    assert plan([(4096, 4096), (1024, 4096), (1024, 4096)], bits=8, gs=128) == ([4, 4, 4], 4, 2)  # 1536 block-tiles
     assert plan([(8192, 8192)]) == ([4], 8, 2)                  # K >= 8192, 1024 tiles of 8 rows: 8-row split
     assert plan([(8192, 8192), (1024, 8192), (1024, 8192)]) == ([4, 4, 4], 8, 2)
     assert plan([(4096, 8192)]) == ([1], 4, 4)                  # 512 tiles of 8 rows: the 4-row rule

@@ -941,10 +941,11 @@ def test_weights_past_two_gib_run_as_row_slices(torch_gpu, m):
 
 
 @pytest.mark.parametrize("bits,gs,sym,n,k,plan", [
-    (4, 128, False, 2044, 4096, ([2], 4, 2)),   # 511 four-row tiles: the K split stays
+    (4, 128, False, 2044, 4096, ([2], 4, 8)),   # 511 four-row tiles: the K split stays (pipelined)
     (4, 128, False, 2048, 4096, ([1], 4, 4)),   # 512: one-wave tiles, pipelined
     (4, 128, False, 4096, 4096, ([1], 4, 4)),   # 1024: the last one-wave size
-    (4, 128, False, 4100, 4096, ([2], 4, 2)),   # 1025: the K split again
+    (4, 128, False, 4100, 4096, ([2], 4, 8)),   # 1025: the K split again (513 block-tiles)
+    (4, 128, False, 8200, 4096, ([2], 4, 2)),   # 2050 tiles x 2 waves: gemv_m1_kernel's split
     (4, 128, False, 8184, 8192, ([4], 4, 2)),   # K = 8192, 1023 eight-row tiles: four-row split
     (4, 128, False, 8192, 8192, ([4], 8, 2)),   # 1024 eight-row tiles: eight-row split
     (2, 64, False, 2044, 14336, ([4], 4, 2)),   # INT2 under 512 tiles: split
