@@ -757,6 +757,54 @@ def test_pipelined_m1_kernel_walk(torch_gpu, bits, gs, sym, layout, shapes, rows
         assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
 
 
+@pytest.mark.parametrize("bits,gs,sym,layout,shapes,wk", [
+    # INT4 g128 asym: two K shares of one batch each, three problems
+    (4, 128, False, "sequential", [(600, 4096), (500, 4096), (300, 4096)], 2),
+    # INT4 g128 asym: four shares of 112 columns (a full and a 48-column
+    # batch each), ragged row counts
+    (4, 128, False, "sequential", [(500, 14336), (262, 14336)], 4),
+    # INT4 g32 sym interleaved: four shares of 40 columns (one partial
+    # batch), a one-row problem
+    (4, 32, True, "interleaved", [(600, 5120), (333, 5120), (1, 5120)], 4),
+    # INT8 g128 sym interleaved and per-channel sym: four shares of 48 columns
+    (8, 128, True, "interleaved", [(700, 3072), (333, 3072)], 4),
+    (8, None, True, "sequential", [(700, 3072), (333, 3072)], 4),
+])
+def test_pipelined_split_walk(torch_gpu, bits, gs, sym, layout, shapes, wk):
+    """gemv_m1_pipe_split_kernel (kind 8 of dq_gemv_plan): the pipelined walk
+    over K shares, the block staging every share's activations, the shares'
+    sums meeting in LDS at each tile's end, crossing problems. Every problem
+    against the oracle on a sample of rows that includes its last 40, against
+    a second launch (bit-equal) and against its single call."""
+    torch = torch_gpu
+    from dequant_project_amd.packer import QuantConfig, quantize_tensor
+
+    assert _plan(shapes, bits, gs) == ([wk] * len(shapes), 4, 8)
+    gen = torch.Generator(device="cuda").manual_seed(bits * 13 + len(shapes) + wk)
+    cfg = QuantConfig(bits, gs, sym, layout)
+    pws, cases, xs, x16s = [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        pw = quantize_tensor(torch.randn(n, k, generator=gen, device="cuda", dtype=torch.float16) * 0.02, cfg)
+        rng = np.random.Generator(np.random.PCG64(900 + i))
+        rows = np.unique(np.concatenate([rng.choice(n, min(n, 160), replace=False), np.arange(max(0, n - 40), n)]))
+        qw, sc = pw.qweight.cpu().numpy(), pw.scales.cpu().numpy()
+        ze = None if pw.zeros is None else pw.zeros.cpu().numpy()
+        cases.append(OracleCase(pw, qw, sc, ze, rows, deq_ref=False))
+        x16s.append(activations(1, k, seed=950 + i))
+        xs.append(to_gpu(torch, x16s[-1]))
+        pws.append(pw)
+    args = ([p.qweight for p in pws], [p.scales for p in pws], [p.zeros for p in pws], bits,
+            [p.config.effective_group_size(p.shape[1]) for p in pws], sym, layout == "interleaved")
+    ys = ext().gemv_batched(xs, *args)
+    again = ext().gemv_batched(xs, *args)
+    for i, (x, pw) in enumerate(zip(xs, pws)):
+        assert torch.equal(ys[i], again[i]), f"problem {i}: not deterministic"
+        cases[i].check(ys[i].cpu().numpy(), x16s[i], f"split walk INT{bits} {shapes[i]} problem {i}")
+        single = ext().gemv(x, *ext_args(pw)).float()
+        diff = (ys[i].float() - single).norm() / single.norm().clamp_min(1e-30)
+        assert diff <= GROUPED_VS_SINGLE_REL_L2, f"problem {i}: grouped vs single rel-L2 {float(diff):.2e}"
+
+
 @pytest.mark.parametrize("bits,gs,sym,layout,shapes,rows_per_tile,m", [
     # the pipelined M = 1 walk's launches (one-wave tiles) at 2 batch rows:
     # ragged rows, partial last batches, a one-row problem (INT4 g32, 8-row tiles)
