@@ -441,6 +441,7 @@ def test_config_c3_int2_asym_g64_outliers(torch_gpu):
     ("C4 gate/up", 14336, 4096, (4, 128, False, "sequential")),
     ("C4 down", 4096, 14336, (4, 128, False, "sequential")),
     ("C5 q/o", 8192, 8192, (4, 128, False, "sequential")),
+    ("C5 k/v", 1024, 8192, (4, 128, False, "sequential")),
     ("C5 gate/up", 28672, 8192, (2, 64, False, "sequential")),
     ("C5 down", 8192, 28672, (2, 64, False, "sequential")),
 ])
@@ -452,7 +453,9 @@ def test_config_layer_shapes(torch_gpu, name, n, k, fmt):
     check_gemv(torch, pw, qw, sc, ze, [activations(m, k, seed=m) for m in (1, 2, 4, 8)], name, rows=rows)
 
 
-def test_config_c5_lm_head_int8_sampled(torch_gpu):
+def test_config_c5_lm_head_int8(torch_gpu):
+    """The 70B lm_head (128256 x 8192, INT8 per channel): 512 sampled rows
+    against the oracle, then every row against the same criterion."""
     torch = torch_gpu
     n, k = 128256, 8192
     from dequant_project_amd.packer import QuantConfig, quantize_tensor
@@ -465,14 +468,33 @@ def test_config_c5_lm_head_int8_sampled(torch_gpu):
     qw = pw.qweight[torch.from_numpy(rows).cuda()].cpu().numpy()
     sc = pw.scales[torch.from_numpy(rows).cuda()].cpu().numpy()
     x16 = activations(1, k, seed=12)
-    y = ext().gemv(to_gpu(torch, x16), *ext_args(pw)).cpu().numpy()[:, rows]
+    y = ext().gemv(to_gpu(torch, x16), *ext_args(pw)).cpu().numpy()
     cfg = P.Config(8, None, True)
     ew = P.exact_weight(qw, sc, None, cfg, (len(rows), k))
     ref, absref = P.gemv_reference(x16, ew)
-    ok, worst = P.gemv_criterion(y, ref, absref)
+    ok, worst = P.gemv_criterion(y[:, rows], ref, absref)
     assert ok, worst
-    assert P.rel_l2(y, x16.astype(np.float32) @ P.dequantize(qw, sc, None, cfg, (len(rows), k))
+    assert P.rel_l2(y[:, rows], x16.astype(np.float32) @ P.dequantize(qw, sc, None, cfg, (len(rows), k))
                     .astype(np.float32).T) <= REL_L2_TOL
+    # Every row, against the same criterion in float64 on the GPU. INT8
+    # sequential words hold codes 4j..4j+3 in bytes 0..3, so the uint8 view of
+    # a row is its codes in order; the exact weight is (q - 128) * s, checked
+    # bit for bit against the oracle's on the sampled rows.
+    xd = torch.from_numpy(x16.astype(np.float64)).cuda()
+    codes = pw.qweight.view(torch.uint8).view(n, k)
+    sd = pw.scales.double()
+    assert torch.equal((codes[torch.from_numpy(rows).cuda()].double() - 128) * sd[torch.from_numpy(rows).cuda()],
+                       torch.from_numpy(ew.astype(np.float64)).cuda())
+    yd = torch.from_numpy(y.astype(np.float64)).cuda()
+    worst_all = 0.0
+    for r0 in range(0, n, 16384):
+        w = (codes[r0:r0 + 16384].double() - 128) * sd[r0:r0 + 16384]
+        ref_c, abs_c = xd @ w.T, xd.abs() @ w.abs().T
+        tol = 2.0 ** -11 * ref_c.abs() + 2.0 ** -20 * abs_c
+        err = (yd[:, r0:r0 + 16384] - ref_c).abs()
+        worst_all = max(worst_all, float((err / (tol + 1e-30)).max()))
+        assert bool((err <= tol).all()), (r0, worst_all)
+        del w
 
 
 # ----------------------------------------------------------- errors (3b)
