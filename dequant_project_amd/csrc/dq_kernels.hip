@@ -1500,6 +1500,13 @@ __device__ __forceinline__ float quad_column_sum(float v) {
 // chunk taken (one more MFMA chain against ones) only in steps where a wave
 // has such a row; every other row subtracts 0 * 0. A row's result does not
 // depend on the other rows' zero points.
+// The tile's problem descriptor is copied into registers when the walk
+// reaches the tile: indexed by the step's problem instead, its fields were
+// read back from the kernel arguments every step, five scalar-load round
+// trips per step (C2 at M = 4: 13.5 -> 12.8-12.9 us per call, the C4 M = 8
+// stack 1-4% faster). The M = 1 walks keep indexing: there the compiler
+// placed the loop-carried copy in LDS (10 -> 20 KiB per block) and they ran
+// about four times slower.
 template <int NT>
 struct QuadAddr {
   __amdgpu_buffer_rsrc_t wbuf, sbuf, zbuf;
@@ -1610,14 +1617,15 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
   if (bt >= total) return;  // block-uniform: the whole block leaves
   int p = 0;
   TilePos t = locate(b, bt, wave, 4 * NT, p);
+  KernelProblem dc = b.p[p];  // the tile's problem, held across its steps (reloaded when the walk moves on)
   int s = 0, par = 0, phase = 0;
   QuadAddr<NT> a;
   u32x4 st[QS::kPerLane];
   uint32_t zb[NT], sb[NT];
   u32x4 w[NT];
   // the first step: activations staged, quads in flight
-  stage_issue<BITS, MG, WK>(b.p[t.p], b.M, s, st);
-  quad_addr<BITS, SYM, NT>(b.p[t.p], t, s, blk, q, true, a);
+  stage_issue<BITS, MG, WK>(dc, b.M, s, st);
+  quad_addr<BITS, SYM, NT>(dc, t, s, blk, q, true, a);
 #pragma unroll
   for (int g = 0; g < NT; ++g) {
     quad_issue<SYM, NT>(a, g, zb[g], sb[g], w[g]);
@@ -1633,14 +1641,18 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
   for (;;) {
     // the next step: the next 16 chunk columns of this tile, or the first
     // step of the next block-tile (the same for the whole block)
-    const int nsteps = b.p[t.p].per_wave >> 4;
+    const int nsteps = dc.per_wave >> 4;
     int ns = s + 1, nbt = bt, np = p;
     TilePos nt = t;
+    KernelProblem dn = dc;
     const bool tile_end = ns >= nsteps;
     if (tile_end) {
       ns = 0;
       nbt = bt + static_cast<int>(gridDim.x);
-      if (nbt < total) nt = locate(b, nbt, wave, 4 * NT, np);
+      if (nbt < total) {
+        nt = locate(b, nbt, wave, 4 * NT, np);
+        dn = b.p[np];
+      }
     }
     const bool nvalid = nbt < total;  // block-uniform
     // the current step's activation pairs
@@ -1660,8 +1672,8 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
       for (int j = 0; j < 4; ++j) x_pairs_from_dwords<BITS, INTER>(xd + j * (F::PER / 2), xp[mg] + j * F::PAIRS);
     }
     // the next step's activations, then its quads as the current ones free their registers
-    if (nvalid) stage_issue<BITS, MG, WK>(b.p[np], b.M, ns, st);
-    quad_addr<BITS, SYM, NT>(b.p[np], nt, ns, blk, q, nvalid, a);
+    if (nvalid) stage_issue<BITS, MG, WK>(dn, b.M, ns, st);
+    quad_addr<BITS, SYM, NT>(dn, nt, ns, blk, q, nvalid, a);
     __builtin_amdgcn_sched_barrier(0);
     // zero points outside [-1024, 1024] in any of the wave's rows of this
     // step (a wave-wide vote): sum(x) per chunk for their z * sum(x) term
@@ -1696,7 +1708,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
         for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
           for (int i = 0; i < 4; ++i) tot[(g * MG + mg) * 4 + i] = quad_column_sum(acc[g][mg][i]);
-      const KernelProblem& d = b.p[t.p];
+      const KernelProblem& d = dc;
       // value v = (g, mg, i) is y[4 mg + i][row0 + 4 g + q]; lane (b = v % 4, q) of row 0 stores it
       if (t.wk == 1) {
 #pragma unroll
@@ -1736,6 +1748,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBat
     bt = nbt;
     p = np;
     t = nt;
+    dc = dn;
   }
 }
 
