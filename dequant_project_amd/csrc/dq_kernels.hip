@@ -1022,6 +1022,29 @@ __device__ __forceinline__ void pair_stage_read(const unsigned char* buf, int la
   }
 }
 
+// The descriptor fields the M = 1 walks read per batch, copied one by one
+// when a walk reaches a tile, so that they stay in registers across its
+// batches (indexed by the batch's problem instead, they are read back from
+// the kernel arguments every batch). A whole-struct copy carried around the
+// loop left the fields the walk never reads in a stack slot, which the
+// compiler then placed in LDS (10 -> 20 KiB per block, written and read
+// every batch).
+__device__ __forceinline__ void take_problem(KernelProblem& dst, const KernelProblem& src) {
+  dst.qweight = src.qweight;
+  dst.scales = src.scales;
+  dst.zeros = src.zeros;
+  dst.x = src.x;
+  dst.y = src.y;
+  dst.aux = src.aux;
+  dst.N = src.N;
+  dst.K = src.K;
+  dst.n_groups = src.n_groups;
+  dst.chunks_per_group = src.chunks_per_group;
+  dst.cpg_shift = src.cpg_shift;
+  dst.n_chunks = src.n_chunks;
+  dst.per_wave = src.per_wave;
+}
+
 // PRO = kProRmsNorm: the staging threads apply the RMSNorm prologue to the
 // words they stage (x * gamma, and their fp32 sum(x^2) accumulated over the
 // tile's batches: every activation of the tile's K is staged once per
@@ -1050,6 +1073,8 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
   int bt = static_cast<int>(blockIdx.x);
   if (bt >= total) return;  // block-uniform: the whole block leaves
   TilePos t = locate(b, bt, wave, R, p);
+  KernelProblem dc;  // the tile's problem (take_problem)
+  take_problem(dc, b.p[p]);
   int cb = t.cb;
   int par = 0;
   BatchAddr<R> a;
@@ -1057,9 +1082,9 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
   uint32_t z[R], s[R];
   u32x4 w[R];
   // the first batch: activations staged, rows in flight
-  pair_stage_issue<BITS>(b.p[t.p].x, b.p[t.p], cb, t.ce, true, raw);
-  if constexpr (RMS || SWI) pair_stage_issue<BITS>(b.p[t.p].aux, b.p[t.p], cb, t.ce, true, gam);
-  batch_addr<BITS, SYM, R>(b.p[t.p], t.row0, cb, t.ce, lane, t.active, a);
+  pair_stage_issue<BITS>(dc.x, dc, cb, t.ce, true, raw);
+  if constexpr (RMS || SWI) pair_stage_issue<BITS>(dc.aux, dc, cb, t.ce, true, gam);
+  batch_addr<BITS, SYM, R>(dc, t.row0, cb, t.ce, lane, t.active, a);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     issue_row<SYM, R>(a, r, z[r], s[r], w[r]);
@@ -1078,12 +1103,15 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     int ncb = cb + 64;
     int nbt = bt, np = p;
     TilePos nt = t;
+    KernelProblem dn;
+    take_problem(dn, dc);
     const bool tile_end = ncb >= t.ce;
     if (tile_end) {
       nbt = bt + static_cast<int>(gridDim.x);
       if (nbt < total) {
         nt = locate(b, nbt, wave, R, np);
         ncb = nt.cb;
+        take_problem(dn, b.p[np]);
       }
     }
     const bool nvalid = nbt < total;  // block-uniform
@@ -1095,9 +1123,9 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     if constexpr (SYM) C = __builtin_fmaf(static_cast<float>(F::BIAS), S, C);
     // the next batch's activations (issued first: vmcnt retires in order),
     // then its rows as the current ones free their registers
-    pair_stage_issue<BITS>(b.p[np].x, b.p[np], ncb, nt.ce, nvalid, raw);
-    if constexpr (RMS || SWI) pair_stage_issue<BITS>(b.p[np].aux, b.p[np], ncb, nt.ce, nvalid, gam);
-    batch_addr<BITS, SYM, R>(b.p[np], nt.row0, ncb, nt.ce, lane, nvalid && nt.active, a);
+    pair_stage_issue<BITS>(dn.x, dn, ncb, nt.ce, nvalid, raw);
+    if constexpr (RMS || SWI) pair_stage_issue<BITS>(dn.aux, dn, ncb, nt.ce, nvalid, gam);
+    batch_addr<BITS, SYM, R>(dn, nt.row0, ncb, nt.ce, lane, nvalid && nt.active, a);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -1118,13 +1146,13 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
         wave_sum_lane63<1>(sq);
         if (lane == 63) rms_part[wave] = sq[0];
         lds_barrier();  // every wave of the block ends its tile here
-        const float f = inv_rms(rms_part[0] + rms_part[1] + rms_part[2] + rms_part[3], b.p[t.p].K, b.eps);
+        const float f = inv_rms(rms_part[0] + rms_part[1] + rms_part[2] + rms_part[3], dc.K, b.eps);
 #pragma unroll
         for (int i = 0; i < R / 4; ++i) yacc[i] *= f;
         ssq = 0.f;
       }
       if (t.active && (lane & 15) == 15)
-        store_rows<R / 4>(b.p[t.p].y, t.row0 + (lane >> 4) * (R / 4), b.p[t.p].N, yacc);
+        store_rows<R / 4>(dc.y, t.row0 + (lane >> 4) * (R / 4), dc.N, yacc);
 #pragma unroll
       for (int r = 0; r < R; ++r) yacc[r] = 0.f;
     }
@@ -1138,6 +1166,7 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     bt = nbt;
     p = np;
     t = nt;
+    take_problem(dc, dn);
   }
 }
 
@@ -1170,6 +1199,8 @@ gemv_m1_pipe_split_kernel(const KernelBatch b) {
   int bt = static_cast<int>(blockIdx.x);
   if (bt >= total) return;  // block-uniform: the whole block leaves
   TilePos t = locate(b, bt, wave, R, p);
+  KernelProblem dc;  // the tile's problem (take_problem)
+  take_problem(dc, b.p[p]);
   int j = 0;  // batch of the current tile (block-uniform)
   int par = 0, phase = 0;
   BatchAddr<R> a;
@@ -1189,8 +1220,8 @@ gemv_m1_pipe_split_kernel(const KernelBatch b) {
     for (int sh = 0; sh < WK; ++sh) pair_stage_write<BITS, INTER>(xs + (pa * WK + sh) * PS::kBufBytes, raw[sh]);
   };
   // the first batch: activations staged, rows in flight
-  stage_issue(b.p[t.p], 0, true);
-  batch_addr<BITS, SYM, R>(b.p[t.p], t.row0, t.cb, t.ce, lane, t.active, a);
+  stage_issue(dc, 0, true);
+  batch_addr<BITS, SYM, R>(dc, t.row0, t.cb, t.ce, lane, t.active, a);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     issue_row<SYM, R>(a, r, z[r], s[r], w[r]);
@@ -1204,14 +1235,19 @@ gemv_m1_pipe_split_kernel(const KernelBatch b) {
   for (;;) {
     // where the next batch is: batch j + 1 of this tile, or the first batch
     // of the next block-tile (the same for the whole block)
-    const int nb = (b.p[t.p].per_wave + 63) >> 6;
+    const int nb = (dc.per_wave + 63) >> 6;
     int nj = j + 1, nbt = bt, np = p;
     TilePos nt = t;
+    KernelProblem dn;
+    take_problem(dn, dc);
     const bool tile_end = nj >= nb;
     if (tile_end) {
       nj = 0;
       nbt = bt + static_cast<int>(gridDim.x);
-      if (nbt < total) nt = locate(b, nbt, wave, R, np);
+      if (nbt < total) {
+        nt = locate(b, nbt, wave, R, np);
+        take_problem(dn, b.p[np]);
+      }
     }
     const bool nvalid = nbt < total;  // block-uniform
     h2 xr[4][F::PAIRS];
@@ -1219,8 +1255,8 @@ gemv_m1_pipe_split_kernel(const KernelBatch b) {
     float S, C;
     bias_sums<BITS>(xr, S, C);
     if constexpr (SYM) C = __builtin_fmaf(static_cast<float>(F::BIAS), S, C);
-    stage_issue(b.p[np], nj, nvalid);
-    batch_addr<BITS, SYM, R>(b.p[np], nt.row0, nt.cb + 64 * nj, nt.ce, lane, nvalid && nt.active, a);
+    stage_issue(dn, nj, nvalid);
+    batch_addr<BITS, SYM, R>(dn, nt.row0, nt.cb + 64 * nj, nt.ce, lane, nvalid && nt.active, a);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -1247,7 +1283,7 @@ gemv_m1_pipe_split_kernel(const KernelBatch b) {
           for (int sh = 0; sh < WK; ++sh) v += part[phase][wave + sh][g * Q + i];
           o[i] = v;
         }
-        store_rows<Q>(b.p[t.p].y, t.row0 + g * Q, b.p[t.p].N, o);
+        store_rows<Q>(dc.y, t.row0 + g * Q, dc.N, o);
       }
       phase ^= 1;
 #pragma unroll
@@ -1261,6 +1297,7 @@ gemv_m1_pipe_split_kernel(const KernelBatch b) {
     bt = nbt;
     p = np;
     t = nt;
+    take_problem(dc, dn);
   }
 }
 
