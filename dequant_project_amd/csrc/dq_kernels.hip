@@ -1541,9 +1541,8 @@ __device__ __forceinline__ float quad_column_sum(float v) {
 // reaches the tile: indexed by the step's problem instead, its fields were
 // read back from the kernel arguments every step, five scalar-load round
 // trips per step (C2 at M = 4: 13.5 -> 12.8-12.9 us per call, the C4 M = 8
-// stack 1-4% faster). The M = 1 walks keep indexing: there the compiler
-// placed the loop-carried copy in LDS (10 -> 20 KiB per block) and they ran
-// about four times slower.
+// stack 1-4% faster). (The M = 1 walks copy field by field instead, see
+// take_problem: a whole-struct copy placed their unread fields in LDS.)
 template <int NT>
 struct QuadAddr {
   __amdgpu_buffer_rsrc_t wbuf, sbuf, zbuf;
