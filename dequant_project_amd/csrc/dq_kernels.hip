@@ -1970,12 +1970,16 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_mfma_kernel(const GemmBatch b
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
         xrow[mb] = static_cast<uint32_t>(min(16 * mb + r, b.M - 1)) * static_cast<uint32_t>(d.K) * 2u;
+      // the fields the iterations read, as values (read through d, the group
+      // fields were loaded from the kernel arguments, and waited on, every
+      // iteration)
+      const int n_chunks = d.n_chunks, n_groups = d.n_groups, cpg_shift = d.cpg_shift, cpg = d.cpg;
       for (int t = ib; t < ie; ++t) {
         const int c = 4 * t + kb;
-        const bool cok = c < d.n_chunks;
-        const uint32_t g = d.n_groups == 1 ? 0u
-                           : (d.cpg_shift >= 0 ? static_cast<uint32_t>(c) >> d.cpg_shift
-                                               : static_cast<uint32_t>(c) / static_cast<uint32_t>(d.cpg));
+        const bool cok = c < n_chunks;
+        const uint32_t g = n_groups == 1 ? 0u
+                           : (cpg_shift >= 0 ? static_cast<uint32_t>(c) >> cpg_shift
+                                             : static_cast<uint32_t>(c) / static_cast<uint32_t>(cpg));
         const uint32_t zb = SYM ? 0u
                                 : __builtin_amdgcn_raw_buffer_load_b16(zbuf, cok ? mrow + g * 2u : kOutOfRange, 0, 0);
         const uint32_t sb = __builtin_amdgcn_raw_buffer_load_b16(sbuf, cok ? mrow + g * 2u : kOutOfRange, 0, 0);
@@ -1993,7 +1997,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_mfma_kernel(const GemmBatch b
             for (int q = 0; q < 4; ++q) {
               const int cq = 4 * t + q;
               xv[mb][q] = __builtin_amdgcn_raw_buffer_load_b128(
-                  xbuf, cq < d.n_chunks ? xrow[mb] + static_cast<uint32_t>(cq) * 64u + 16u * kb : kOutOfRange, 0, 0);
+                  xbuf, cq < n_chunks ? xrow[mb] + static_cast<uint32_t>(cq) * 64u + 16u * kb : kOutOfRange, 0, 0);
             }
           }
 #pragma unroll
@@ -2125,9 +2129,13 @@ __global__ void __launch_bounds__(256 * TPB) gemm_shared_x_kernel(const GemmBatc
     const __amdgpu_buffer_rsrc_t xbuf = buffer_of(d.x, static_cast<uint32_t>(b.M) * kbytes);
     const uint32_t n = static_cast<uint32_t>(min(row0 + r, d.N - 1));  // past N: re-read, never stored
     const uint32_t wrow = n * row_bytes, mrow = n * meta_row;
+    // the fields the iterations read, as values (read through d, they were
+    // loaded from the kernel arguments, and waited on, every iteration)
+    const int per_wave = d.per_wave, n_chunks = d.n_chunks, n_groups = d.n_groups, cpg_shift = d.cpg_shift,
+              cpg = d.cpg;
     // every wave, active or not, runs every iteration of the block's problem
     // (the K-shares stage together and meet at each iteration's barrier)
-    for (int t = 0; t < d.per_wave; ++t) {
+    for (int t = 0; t < per_wave; ++t) {
       unsigned char* buf = xs_lds + parity * SX::kBufBytes;
       parity ^= 1;
       const bool iok = ib + t < ie;
@@ -2138,17 +2146,17 @@ __global__ void __launch_bounds__(256 * TPB) gemm_shared_x_kernel(const GemmBatc
         const int e = tk + SX::kShareThreads * i;
         const int piece = e % SX::kPieces, cc = (e / SX::kPieces) % 4, m = e / (SX::kPieces * 4);
         const int c = 4 * (ib + t) + cc;
-        const bool ok = e < SX::kPieceCount && iok && m < b.M && c < d.n_chunks;
+        const bool ok = e < SX::kPieceCount && iok && m < b.M && c < n_chunks;
         st[i] = __builtin_amdgcn_raw_buffer_load_b128(
             xbuf, ok ? static_cast<uint32_t>(m) * kbytes + static_cast<uint32_t>(c) * SX::kChunkBytes + 16u * piece
                      : kOutOfRange,
             0, 0);
       }
       const int c = 4 * (ib + t) + kb;
-      const bool cok = active && iok && c < d.n_chunks;
-      const uint32_t g = d.n_groups == 1 ? 0u
-                         : (d.cpg_shift >= 0 ? static_cast<uint32_t>(c) >> d.cpg_shift
-                                             : static_cast<uint32_t>(c) / static_cast<uint32_t>(d.cpg));
+      const bool cok = active && iok && c < n_chunks;
+      const uint32_t g = n_groups == 1 ? 0u
+                         : (cpg_shift >= 0 ? static_cast<uint32_t>(c) >> cpg_shift
+                                           : static_cast<uint32_t>(c) / static_cast<uint32_t>(cpg));
       const uint32_t zb = SYM ? 0u : __builtin_amdgcn_raw_buffer_load_b16(zbuf, cok ? mrow + g * 2u : kOutOfRange, 0, 0);
       const uint32_t sb = __builtin_amdgcn_raw_buffer_load_b16(sbuf, cok ? mrow + g * 2u : kOutOfRange, 0, 0);
       const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(
