@@ -309,6 +309,31 @@ __device__ __forceinline__ uint32_t group_of(const KernelProblem& d, int c) {
   return static_cast<uint32_t>(c) / static_cast<uint32_t>(d.chunks_per_group);
 }
 
+// The descriptor fields the M = 1 walks read per batch, copied one by one
+// when a walk reaches a tile, so that they stay in registers across its
+// batches (read through the kernel arguments instead, they were loaded, and
+// waited on, every batch; gemv_mx_pipe_kernel, measured about 1% slower
+// with the copy, keeps indexing). A whole-struct copy carried around the
+// loop left the fields the walk never reads in a stack slot, which the
+// compiler then placed in LDS (10 -> 20 KiB per block, written and read
+// every batch).
+__device__ __forceinline__ void take_problem(KernelProblem& dst, const KernelProblem& src) {
+  dst.qweight = src.qweight;
+  dst.scales = src.scales;
+  dst.zeros = src.zeros;
+  dst.x = src.x;
+  dst.y = src.y;
+  dst.aux = src.aux;
+  dst.N = src.N;
+  dst.K = src.K;
+  dst.n_groups = src.n_groups;
+  dst.chunks_per_group = src.chunks_per_group;
+  dst.cpg_shift = src.cpg_shift;
+  dst.n_chunks = src.n_chunks;
+  dst.per_wave = src.per_wave;
+  dst.ldy = src.ldy;
+}
+
 // The loads of one tile: R rows x CMAX 16-byte chunk columns per lane, plus
 // the rows' fp16 scales (and zeros) of those chunks.
 template <int BITS, int R, int CMAX>
@@ -776,7 +801,9 @@ gemv_m1_kernel(const KernelBatch b) {
   int in_run = 0;
   while (bt < total) {
     const TilePos t = locate(b, bt, wave, R, p);
-    const KernelProblem& d = b.p[t.p];
+    KernelProblem dl;  // the tile's problem (take_problem)
+    take_problem(dl, b.p[t.p]);
+    const KernelProblem& d = dl;
     float yacc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) yacc[r] = 0.f;
@@ -1020,29 +1047,6 @@ __device__ __forceinline__ void pair_stage_read(const unsigned char* buf, int la
 #pragma unroll
     for (int e = 0; e < 4; ++e) xr[(4 * k + e) / F::PAIRS][(4 * k + e) % F::PAIRS] = as_h2(v[e]);
   }
-}
-
-// The descriptor fields the M = 1 walks read per batch, copied one by one
-// when a walk reaches a tile, so that they stay in registers across its
-// batches (indexed by the batch's problem instead, they are read back from
-// the kernel arguments every batch). A whole-struct copy carried around the
-// loop left the fields the walk never reads in a stack slot, which the
-// compiler then placed in LDS (10 -> 20 KiB per block, written and read
-// every batch).
-__device__ __forceinline__ void take_problem(KernelProblem& dst, const KernelProblem& src) {
-  dst.qweight = src.qweight;
-  dst.scales = src.scales;
-  dst.zeros = src.zeros;
-  dst.x = src.x;
-  dst.y = src.y;
-  dst.aux = src.aux;
-  dst.N = src.N;
-  dst.K = src.K;
-  dst.n_groups = src.n_groups;
-  dst.chunks_per_group = src.chunks_per_group;
-  dst.cpg_shift = src.cpg_shift;
-  dst.n_chunks = src.n_chunks;
-  dst.per_wave = src.per_wave;
 }
 
 // PRO = kProRmsNorm: the staging threads apply the RMSNorm prologue to the
