@@ -801,7 +801,7 @@ gemv_m1_kernel(const KernelBatch b) {
   int in_run = 0;
   while (bt < total) {
     const TilePos t = locate(b, bt, wave, R, p);
-    KernelProblem dl;  // the tile's problem (take_problem)
+    KernelProblem dl{};  // the tile's problem (take_problem; the fields it does not copy stay zero)
     take_problem(dl, b.p[t.p]);
     const KernelProblem& d = dl;
     float yacc[R];
@@ -1077,7 +1077,7 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
   int bt = static_cast<int>(blockIdx.x);
   if (bt >= total) return;  // block-uniform: the whole block leaves
   TilePos t = locate(b, bt, wave, R, p);
-  KernelProblem dc;  // the tile's problem (take_problem)
+  KernelProblem dc{};  // the tile's problem (take_problem; the fields it does not copy stay zero)
   take_problem(dc, b.p[p]);
   int cb = t.cb;
   int par = 0;
@@ -1107,7 +1107,7 @@ gemv_m1_pipe_kernel(const KernelBatch b) {
     int ncb = cb + 64;
     int nbt = bt, np = p;
     TilePos nt = t;
-    KernelProblem dn;
+    KernelProblem dn{};
     take_problem(dn, dc);
     const bool tile_end = ncb >= t.ce;
     if (tile_end) {
@@ -1203,7 +1203,7 @@ gemv_m1_pipe_split_kernel(const KernelBatch b) {
   int bt = static_cast<int>(blockIdx.x);
   if (bt >= total) return;  // block-uniform: the whole block leaves
   TilePos t = locate(b, bt, wave, R, p);
-  KernelProblem dc;  // the tile's problem (take_problem)
+  KernelProblem dc{};  // the tile's problem (take_problem; the fields it does not copy stay zero)
   take_problem(dc, b.p[p]);
   int j = 0;  // batch of the current tile (block-uniform)
   int par = 0, phase = 0;
@@ -1242,7 +1242,7 @@ gemv_m1_pipe_split_kernel(const KernelBatch b) {
     const int nb = (dc.per_wave + 63) >> 6;
     int nj = j + 1, nbt = bt, np = p;
     TilePos nt = t;
-    KernelProblem dn;
+    KernelProblem dn{};
     take_problem(dn, dc);
     const bool tile_end = nj >= nb;
     if (tile_end) {
