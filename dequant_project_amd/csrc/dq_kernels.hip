@@ -1636,8 +1636,16 @@ __device__ __forceinline__ void quad_math(const u32x4& w, uint32_t zb, uint32_t 
   }
 }
 
+// Two batch-row groups with one K share (the M = 5..8 launches of large
+// problems, e.g. the C4 stack at M = 8) are asked to fit four waves per SIMD:
+// 125 VGPRs without spills instead of 144 (three waves); the C4 M = 8 stack
+// ran 34.7 / 35.3 -> 34.0 / 33.5 us/layer (same box, two alternations). The
+// other instances keep the compiler's choice: asked the same, the INT2 ones
+// and those with K shares spilled to scratch.
 template <int BITS, bool SYM, bool INTER, int NT, int MG, int WK>
-__global__ void __launch_bounds__(kGemvThreads) gemv_quad_kernel(const KernelBatch b) {
+__global__ void __launch_bounds__(kGemvThreads)
+__attribute__((amdgpu_waves_per_eu(BITS != 2 && MG == 2 && WK == 1 ? 4 : 1, 8)))
+gemv_quad_kernel(const KernelBatch b) {
   using F = Fmt<BITS>;
   using QS = QuadStage<BITS, MG, WK>;
   constexpr int CPL = F::CPL, NF = CPL / 4;
